@@ -1,0 +1,307 @@
+// extern "C" entry points of libforge_mi355x.so: argument validation, per-shape kernel policy, launch.
+// Declarations and the reference interface each one replaces: include/forge_mi355x.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/forge_mi355x.h"
+
+namespace fg {
+hipError_t launch_w4_gemv(int mt, int R, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                          const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                          const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K,
+                          int gs, int max_blocks, hipStream_t s);
+hipError_t launch_w4_generic(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
+                             int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                             const int32_t* g_idx, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                             int K, int gs, hipStream_t s);
+hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+                             const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int odt, int64_t ldo,
+                             int N, int K, int gs, hipStream_t s);
+hipError_t launch_w4_mfma(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                          const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M, int N, int K, int gs,
+                          int tile_m, int splits, hipStream_t s);
+void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchunk, int* used);
+size_t w4_gemv_lds_bytes(int mt, int K);
+hipError_t launch_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                            int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                            int64_t ldy, int ydt, int M, int N, int K, int tile, hipStream_t s);
+hipError_t launch_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
+                           int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
+                           int64_t ldy, int ydt, int M, int N, int K, int tile, hipStream_t s);
+hipError_t launch_fp8_gemm_blocked(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, int64_t sa_sk,
+                                   const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_sn, int64_t sb_sk,
+                                   int sb_div, const void* bias, int bdt, void* y, int64_t ldy, int ydt, int M, int N,
+                                   int K, hipStream_t s);
+hipError_t launch_quant_int8(const void* x, int64_t ldx, int xdt, int8_t* q, int64_t ldq, float* s, int M, int K,
+                             hipStream_t st);
+hipError_t launch_quant_fp8(const void* x, int64_t ldx, int xdt, uint8_t* q, int64_t ldq, float* s, int M, int K,
+                            const float* static_scale, const void* rms_w, int wdt, float eps, int fuse,
+                            hipStream_t st);
+hipError_t launch_quant_fp8_block(const void* x, int64_t ldx, int xdt, uint8_t* q, int64_t ldq, float* s,
+                                  int64_t lds, int M, int K, int bm, int bk, const float* static_scale,
+                                  hipStream_t st);
+}  // namespace fg
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FG_OK;
+  return fail(FG_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool is_float_dt(int dt) { return dt == FG_F32 || dt == FG_F16 || dt == FG_BF16; }
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+}  // namespace
+
+extern "C" {
+
+const char* fg_version(void) { return "forge_mi355x 0.1.0 (gfx950)"; }
+
+const char* fg_last_error(void) { return g_err.c_str(); }
+
+int fg_device_ok(int device) {
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) {
+    fail(FG_EHIP, "hipGetDeviceProperties(%d): %s", device, hipGetErrorString(e));
+    return 0;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    fail(FG_EUNSUPPORTED, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    return 0;
+  }
+  return 1;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
+// workspace a caller sizes is the workspace the launch uses.
+struct W4Plan {
+  int impl;
+  int mt, rows, max_blocks;  // GEMV
+  int tile_m, splits;        // MFMA
+  size_t ws_bytes;
+};
+
+int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned, bool q_aligned, bool has_g_idx,
+            const fg_w4_config* cfg, W4Plan* p) {
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int impl = cfg ? cfg->impl : FG_W4_AUTO;
+  const bool gemv_ok = !has_g_idx && q_aligned && (gs % 32 == 0 || group_size <= 0) && M <= 4 &&
+                       fg::w4_gemv_lds_bytes(4, (int)K) <= 150 * 1024;
+  const bool mfma_ok = !has_g_idx && q_aligned && x_aligned && (K % 8 == 0);
+  int use = impl;
+  if (use == FG_W4_AUTO) use = gemv_ok ? FG_W4_GEMV : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC);
+  if (use == FG_W4_GEMV && !gemv_ok)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: GEMV needs M<=4, no g_idx, group%%32==0, ldq%%4==0, aligned qweight");
+  if (use == FG_W4_MFMA && !mfma_ok)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: MFMA path needs no g_idx, K%%8==0, ldq%%4==0, ldx%%8==0 and "
+                                 "16-byte aligned x/qweight");
+  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC)
+    return fail(FG_EINVAL, "fg_w4a16_gemm: unknown impl %d", impl);
+  *p = W4Plan{use, 1, 4, 0, 0, 1, 0};
+  if (use == FG_W4_GEMV) {
+    p->mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    p->rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 4;
+    if (p->rows != 1 && p->rows != 2 && p->rows != 4) return fail(FG_EINVAL, "fg_w4a16_gemm: rows_per_wave must be 1, 2 or 4");
+    p->max_blocks = cfg ? cfg->max_blocks : 0;
+  } else if (use == FG_W4_MFMA) {
+    p->tile_m = cfg ? cfg->tile_m : 0;
+    int kchunk = 0, used = 1;
+    fg::w4_mfma_split_plan((int)M, (int)N, (int)K, p->tile_m, cfg ? cfg->split_k : 0, &kchunk, &used);
+    p->splits = cfg && cfg->split_k ? cfg->split_k : 0;
+    p->ws_bytes = used > 1 ? (size_t)used * (size_t)M * (size_t)N * sizeof(float) : 0;
+  }
+  return FG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t x_aligned,
+                                int32_t q_aligned, int32_t has_g_idx, const fg_w4_config* cfg) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+  W4Plan p;
+  if (plan_w4(M, N, K, group_size, x_aligned != 0, q_aligned != 0, has_g_idx != 0, cfg, &p) != FG_OK) return 0;
+  return p.ws_bytes;
+}
+
+int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq, const void* scales,
+                  int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                  const int32_t* g_idx, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                  int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
+                  size_t workspace_bytes, fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_w4a16_gemm: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (M == 0) return FG_OK;
+  if (x_dtype != FG_BF16 && x_dtype != FG_F16) return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: x must be bf16 or fp16");
+  if (!is_float_dt(scale_dtype)) return fail(FG_EINVAL, "fg_w4a16_gemm: bad scale dtype %d", scale_dtype);
+  if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_w4a16_gemm: bad bias dtype %d", bias_dtype);
+  if (!x || !qweight || !scales || !y) return fail(FG_EINVAL, "fg_w4a16_gemm: null tensor");
+  const int64_t KW = (K + 7) / 8;
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int64_t G = (K + gs - 1) / gs;
+  if (group_size > 0 && group_size % 8 != 0)
+    return fail(FG_EINVAL, "fg_w4a16_gemm: group_size must be a multiple of 8 or <= 0, got %d", group_size);
+  if (ldq < KW || lds < N || ldx < K || ldy < N || (zeros && ldz < (N + 7) / 8))
+    return fail(FG_EINVAL, "fg_w4a16_gemm: leading dimensions too small");
+  if (n_groups <= 0 || (!g_idx && n_groups < G))
+    return fail(FG_EINVAL, "fg_w4a16_gemm: n_groups=%d does not cover K=%lld with group %d", n_groups, (long long)K, gs);
+
+  const bool x_aligned = (ldx % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  const bool q_aligned = (ldq % 4 == 0) && (reinterpret_cast<uintptr_t>(qweight) % 16 == 0);
+  W4Plan p;
+  const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, &p);
+  if (rc != FG_OK) return rc;
+  if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes))
+    return fail(FG_EINVAL, "fg_w4a16_gemm: workspace of %zu bytes needed, %zu given", p.ws_bytes,
+                workspace ? workspace_bytes : (size_t)0);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool xbf16 = x_dtype == FG_BF16;
+  hipError_t e;
+  if (p.impl == FG_W4_GEMV) {
+    e = fg::launch_w4_gemv(p.mt, p.rows, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
+                           bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, p.max_blocks, s);
+  } else if (p.impl == FG_W4_MFMA) {
+    e = fg::launch_w4_mfma(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias, bias_dtype,
+                           y, ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, p.tile_m, p.splits, s);
+  } else {
+    e = fg::launch_w4_generic(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias,
+                              bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, s);
+  }
+  return hip_status(e, "fg_w4a16_gemm launch");
+}
+
+int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int scale_dtype, int64_t lds,
+                  const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int out_dtype, int64_t ldo,
+                  int64_t N, int64_t K, int32_t group_size, int32_t n_groups, fg_stream_t stream) {
+  if (N <= 0 || K <= 0 || N >= kMaxDim || K >= kMaxDim) return fail(FG_EINVAL, "fg_w4_dequant: bad sizes");
+  if (!qweight || !scales || !out) return fail(FG_EINVAL, "fg_w4_dequant: null tensor");
+  if (!is_float_dt(scale_dtype) || !is_float_dt(out_dtype)) return fail(FG_EINVAL, "fg_w4_dequant: bad dtype");
+  const int gs = group_size > 0 ? group_size : (int)K;
+  if (group_size > 0 && group_size % 8 != 0) return fail(FG_EINVAL, "fg_w4_dequant: group_size must be a multiple of 8");
+  if (ldq < (K + 7) / 8 || lds < N || ldo < K || (zeros && ldz < (N + 7) / 8))
+    return fail(FG_EINVAL, "fg_w4_dequant: leading dimensions too small");
+  if (n_groups <= 0 || (!g_idx && n_groups < (K + gs - 1) / gs))
+    return fail(FG_EINVAL, "fg_w4_dequant: n_groups does not cover K");
+  return hip_status(fg::launch_w4_dequant(qweight, ldq, scales, scale_dtype, lds, zeros, ldz, g_idx, out, out_dtype,
+                                          ldo, (int)N, (int)K, gs, static_cast<hipStream_t>(stream)),
+                    "fg_w4_dequant launch");
+}
+
+int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b, int64_t ldb,
+                 const float* sb, int64_t sb_len, const void* bias, int bias_dtype, void* y, int64_t ldy, int y_dtype,
+                 int64_t M, int64_t N, int64_t K, const fg_mm_config* cfg, fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_int8_gemm: bad sizes");
+  if (M == 0) return FG_OK;
+  if (!a || !b || !y) return fail(FG_EINVAL, "fg_int8_gemm: null tensor");
+  if (y_dtype != FG_I32) {
+    if (!is_float_dt(y_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad output dtype %d", y_dtype);
+    if (!sa || !sb || (sa_len != 1 && sa_len != M) || (sb_len != 1 && sb_len != N))
+      return fail(FG_EINVAL, "fg_int8_gemm: scale sizes %lld/%lld do not match M=%lld/N=%lld", (long long)sa_len,
+                  (long long)sb_len, (long long)M, (long long)N);
+    if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad bias dtype");
+  }
+  if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
+  const int tile = cfg && cfg->tile_m ? cfg->tile_m : (M <= 64 || N <= 64 ? 64 : 128);
+  return hip_status(fg::launch_int8_gemm(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy, y_dtype,
+                                         (int)M, (int)N, (int)K, tile, static_cast<hipStream_t>(stream)),
+                    "fg_int8_gemm launch");
+}
+
+int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, int64_t sa_sk, const uint8_t* b,
+                int64_t ldb, const float* sb, int64_t sb_sn, int64_t sb_sk, int32_t sb_div, int32_t scale_mode,
+                int32_t block, const void* bias, int bias_dtype, void* y, int64_t ldy, int y_dtype, int64_t M,
+                int64_t N, int64_t K, const fg_mm_config* cfg, fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_fp8_gemm: bad sizes");
+  if (M == 0) return FG_OK;
+  if (!a || !b || !y || !sa || !sb) return fail(FG_EINVAL, "fg_fp8_gemm: null tensor");
+  if (!is_float_dt(y_dtype)) return fail(FG_EINVAL, "fg_fp8_gemm: bad output dtype %d", y_dtype);
+  if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_fp8_gemm: bad bias dtype");
+  if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_fp8_gemm: leading dimensions too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (scale_mode == 0 || scale_mode == 1) {
+    if (scale_mode == 0) sa_sm = sb_sn = 0;
+    const int tile = cfg && cfg->tile_m ? cfg->tile_m : (M <= 64 || N <= 64 ? 64 : 128);
+    return hip_status(fg::launch_fp8_gemm(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy, y_dtype,
+                                          (int)M, (int)N, (int)K, tile, s),
+                      "fg_fp8_gemm launch");
+  }
+  if (scale_mode == 2) {
+    if (block != 128) return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: block scales need block=128, got %d", block);
+    if (sb_div != 1 && sb_div != 128) return fail(FG_EINVAL, "fg_fp8_gemm: sb_div must be 1 or the block");
+    return hip_status(fg::launch_fp8_gemm_blocked(a, lda, sa, sa_sm, sa_sk, b, ldb, sb, sb_sn, sb_sk, sb_div, bias,
+                                                  bias_dtype, y, ldy, y_dtype, (int)M, (int)N, (int)K, s),
+                      "fg_fp8_gemm launch");
+  }
+  return fail(FG_EINVAL, "fg_fp8_gemm: unknown scale_mode %d", scale_mode);
+}
+
+int fg_quant_int8_rowwise(const void* x, int64_t ldx, int x_dtype, int8_t* q, int64_t ldq, float* s, int64_t M,
+                          int64_t K, fg_stream_t stream) {
+  if (M < 0 || K <= 0 || M >= kMaxDim || K >= kMaxDim) return fail(FG_EINVAL, "fg_quant_int8_rowwise: bad sizes");
+  if (M == 0) return FG_OK;
+  if (!x || !q || !s) return fail(FG_EINVAL, "fg_quant_int8_rowwise: null tensor");
+  if (!is_float_dt(x_dtype)) return fail(FG_EINVAL, "fg_quant_int8_rowwise: bad x dtype");
+  if (ldx < K || ldq < K) return fail(FG_EINVAL, "fg_quant_int8_rowwise: leading dimensions too small");
+  return hip_status(fg::launch_quant_int8(x, ldx, x_dtype, q, ldq, s, (int)M, (int)K, static_cast<hipStream_t>(stream)),
+                    "fg_quant_int8_rowwise launch");
+}
+
+int fg_quant_fp8_rowwise(const void* x, int64_t ldx, int x_dtype, uint8_t* q, int64_t ldq, float* s, int64_t M,
+                         int64_t K, const float* static_scale, const void* rms_weight, int rms_weight_dtype,
+                         float rms_eps, int32_t fuse_rmsnorm, fg_stream_t stream) {
+  if (M < 0 || K <= 0 || M >= kMaxDim || K >= kMaxDim) return fail(FG_EINVAL, "fg_quant_fp8_rowwise: bad sizes");
+  if (M == 0) return FG_OK;
+  if (!x || !q || (!s && !static_scale)) return fail(FG_EINVAL, "fg_quant_fp8_rowwise: null tensor");
+  if (!is_float_dt(x_dtype)) return fail(FG_EINVAL, "fg_quant_fp8_rowwise: bad x dtype");
+  if (rms_weight && !is_float_dt(rms_weight_dtype)) return fail(FG_EINVAL, "fg_quant_fp8_rowwise: bad weight dtype");
+  if (ldx < K || ldq < K) return fail(FG_EINVAL, "fg_quant_fp8_rowwise: leading dimensions too small");
+  return hip_status(fg::launch_quant_fp8(x, ldx, x_dtype, q, ldq, s, (int)M, (int)K, static_scale, rms_weight,
+                                         rms_weight_dtype, rms_eps, fuse_rmsnorm, static_cast<hipStream_t>(stream)),
+                    "fg_quant_fp8_rowwise launch");
+}
+
+int fg_quant_fp8_block(const void* x, int64_t ldx, int x_dtype, uint8_t* q, int64_t ldq, float* s, int64_t lds,
+                       int64_t M, int64_t K, int32_t block_m, int32_t block_k, const float* static_scale,
+                       fg_stream_t stream) {
+  if (M < 0 || K <= 0 || M >= kMaxDim || K >= kMaxDim || block_m <= 0 || block_k <= 0)
+    return fail(FG_EINVAL, "fg_quant_fp8_block: bad sizes");
+  if (M == 0) return FG_OK;
+  if (!x || !q || (!s && !static_scale)) return fail(FG_EINVAL, "fg_quant_fp8_block: null tensor");
+  if (!is_float_dt(x_dtype)) return fail(FG_EINVAL, "fg_quant_fp8_block: bad x dtype");
+  const int64_t kb = (K + block_k - 1) / block_k, mb = (M + block_m - 1) / block_m;
+  if (ldx < K || ldq < K || (s && lds < kb)) return fail(FG_EINVAL, "fg_quant_fp8_block: leading dimensions too small");
+  if (kb >= 65536 * 32768LL || mb >= 65536) return fail(FG_EINVAL, "fg_quant_fp8_block: too many blocks");
+  return hip_status(fg::launch_quant_fp8_block(x, ldx, x_dtype, q, ldq, s, lds, (int)M, (int)K, block_m, block_k,
+                                               static_scale, static_cast<hipStream_t>(stream)),
+                    "fg_quant_fp8_block launch");
+}
+
+}  // extern "C"

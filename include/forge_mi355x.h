@@ -1,0 +1,155 @@
+/* forge_mi355x -- C ABI of the MI355X-native (gfx950) quantized-linear hot path.
+ *
+ * One shared library, libforge_mi355x.so, built with hipcc --offload-arch=gfx950.  Every entry point takes plain
+ * device pointers, element strides and sizes, enqueues its kernels on `stream` and returns immediately (no host
+ * synchronisation, no device allocation: callers own every buffer, so launches can be captured in a HIP graph).
+ *
+ * Return value: FG_OK (0) or an error code; fg_last_error() gives a message for the calling thread.
+ *
+ * Each entry point names the reference interface it replaces (paths are in the Forge-LLM source tree).
+ */
+#ifndef FORGE_MI355X_H
+#define FORGE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* fg_stream_t; /* a hipStream_t; NULL = the default stream */
+
+/* element type codes */
+enum {
+  FG_F32 = 0,
+  FG_F16 = 1,
+  FG_BF16 = 2,
+  FG_E4M3 = 3, /* OCP float8 e4m3fn */
+  FG_I8 = 4,
+  FG_I32 = 5
+};
+
+/* status codes */
+enum { FG_OK = 0, FG_EINVAL = 1, FG_EUNSUPPORTED = 2, FG_EHIP = 3 };
+
+/* W4A16 implementation selector (fg_w4_config.impl) */
+enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3 };
+
+/* Launch knobs; pass NULL for the built-in per-shape policy.  Zero fields mean "policy default". */
+typedef struct fg_w4_config {
+  int32_t impl;         /* FG_W4_* */
+  int32_t rows_per_wave; /* GEMV: output channels per wavefront (1, 2 or 4) */
+  int32_t max_blocks;   /* GEMV: cap on workgroups (grid-stride beyond it) */
+  int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128) */
+  int32_t split_k;      /* MFMA: K splits (fp32 partials in the workspace, reduced in fixed order) */
+  int32_t reserved[3];
+} fg_w4_config;
+
+typedef struct fg_mm_config {
+  int32_t tile_m; /* 0 = policy */
+  int32_t tile_n;
+  int32_t reserved[6];
+} fg_mm_config;
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * W4A16:  y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+ bias),  W[n,k] = (q[n,k] - zero[n,g(k)]) * scale[n,g(k)].
+ * Replaces the Triton launchers behind w4a16_linear: forge/kernels/ops_gemm.py:287-317 ->
+ * forge/kernels/triton/gemm_w4a16.py:69-153 (w4a16_gemm_triton), gemm_w4_fast.py:274-343 (w4_fast_gemm, gemv/dot),
+ * gemm_w4_dequant.py:194-236 (w4_dequant_matmul), gemm_wq.py:138-204 (legacy wq_gemm).
+ *   x        x_dtype (FG_BF16 | FG_F16) [M, ldx], unit stride along K
+ *   qweight  int32 [N, ldq] portable_row words (forge/kernels/layouts/w4.py:15-17), ldq >= ceil(K/8)
+ *   scales   scale_dtype (FG_F16 | FG_BF16 | FG_F32) [n_groups, lds], lds >= N
+ *   zeros    int32 [n_groups, ldz] packed 8 channels per word, or NULL (symmetric, zero-point 8)
+ *   perm     int32 [K] or NULL: column order of a group-sorted act-order weight; x is read as x[:, perm[k]]
+ *   g_idx    int32 [K] or NULL: per-column group id (irregular act-order; selects the generic kernel)
+ *   bias     bias_dtype [N] or NULL
+ *   y        x_dtype [M, ldy]
+ *   group_size  > 0 (multiple of 8) or <= 0 for one group per row
+ *   workspace   device scratch of at least fg_w4a16_workspace_bytes(...) bytes (may be NULL when that is 0); the
+ *               caller allocates it (e.g. from the torch caching allocator on the same stream), as the reference's
+ *               split-K workspace (forge/kernels/triton/gemm_w4_fast.py:316-318)
+ * ------------------------------------------------------------------------------------------------------------- */
+int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq, const void* scales,
+                  int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                  const int32_t* g_idx, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                  int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
+                  size_t workspace_bytes, fg_stream_t stream);
+
+/* Workspace bytes fg_w4a16_gemm needs for this problem and config (0 for single-pass launches).  The alignment and
+ * g_idx flags must match the later call: x_aligned = x and ldx allow 16-byte row loads, q_aligned = qweight and ldq
+ * allow 16-byte chunk loads, has_g_idx = a per-column g_idx will be passed. */
+size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t x_aligned,
+                                int32_t q_aligned, int32_t has_g_idx, const fg_w4_config* cfg);
+
+/* Dense dequantisation out[n,k] = (q - z) * s computed in fp32 and rounded once to out_dtype (FG_F32|FG_F16|FG_BF16).
+ * Replaces forge/kernels/triton/gemm_w4_dequant.py:143-191 (w4_dequant) and PackedW4.dequantize
+ * (forge/kernels/layouts/w4.py:137-140 -> dequantize_parts :294-305). */
+int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int scale_dtype, int64_t lds,
+                  const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int out_dtype, int64_t ldo,
+                  int64_t N, int64_t K, int32_t group_size, int32_t n_groups, fg_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * INT8 W8A8:  acc[M,N] = a[M,K] @ b[N,K]^T in exact int32;  y = (float(acc) * sa[m]) * sb[n] (+ bias[n]).
+ * Replaces forge/kernels/triton/gemm_int8.py:95-137 (int8_gemm_triton), called from int8_linear
+ * (forge/kernels/ops_gemm.py:483-515).
+ *   sa  float [sa_len], sa_len in {1, M};  sb float [sb_len], sb_len in {1, N}
+ *   y_dtype  FG_F32 | FG_F16 | FG_BF16, or FG_I32 to store the raw int32 accumulator (scales and bias ignored)
+ * ------------------------------------------------------------------------------------------------------------- */
+int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b, int64_t ldb,
+                 const float* sb, int64_t sb_len, const void* bias, int bias_dtype, void* y, int64_t ldy, int y_dtype,
+                 int64_t M, int64_t N, int64_t K, const fg_mm_config* cfg, fg_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * FP8 W8A8 (OCP e4m3fn operands, fp32 accumulation):  y = sum_k (a*sa)(b*sb) (+ bias).
+ * Replaces forge/kernels/triton/gemm_fp8.py:194-248 (fp8_gemm_triton) with the scale normalisation of
+ * prepare_fp8_scales (gemm_fp8.py:151-191), called from fp8_linear (forge/kernels/ops_gemm.py:396-461).
+ *   scale_mode 0: per-tensor sa[0], sb[0];  1: sa[m * sa_sm], sb[n * sb_sn] (stride 0 broadcasts);
+ *              2: K-blocked: sa[m * sa_sm + kb * sa_sk], sb[(n / sb_div) * sb_sn + kb * sb_sk], kb = k / block
+ *   y_dtype FG_F32 | FG_F16 | FG_BF16
+ * ------------------------------------------------------------------------------------------------------------- */
+int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, int64_t sa_sk, const uint8_t* b,
+                int64_t ldb, const float* sb, int64_t sb_sn, int64_t sb_sk, int32_t sb_div, int32_t scale_mode,
+                int32_t block, const void* bias, int bias_dtype, void* y, int64_t ldy, int y_dtype, int64_t M,
+                int64_t N, int64_t K, const fg_mm_config* cfg, fg_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Per-token activation quantisers (one scale per row of x).
+ * INT8: s = amax /_IEEE 127 (1 if amax is not > 0), q = clamp(round_half_even(x /_IEEE s), -127, 127).
+ *   Replaces forge/kernels/triton/gemm_int8.py:140-151 (int8_quant_triton) behind quantize_act_int8
+ *   (forge/kernels/ops_gemm.py:467-480); oracle forge/kernels/ref/gemm_int8.py:17-35.
+ * FP8:  optional fused RMSNorm y = x * rsqrt(mean(x^2) + eps) * w (fp32), then s = amax / 448 (1 if amax is not > 0),
+ *       q = e4m3fn(clamp(y / s, -448, 448)), round-half-even.  static_scale (device float[M], one per row)
+ *       replaces s when given (s may then be NULL).
+ *   Replaces forge/kernels/triton/gemm_fp8.py:251-304 (act_quant_fp8_triton, per_token / per_tensor-static) behind
+ *   quantize_act_fp8 (forge/kernels/ops_gemm.py:359-388); oracles forge/kernels/ref/gemm_fp8.py:43-85,130-150.
+ * ------------------------------------------------------------------------------------------------------------- */
+int fg_quant_int8_rowwise(const void* x, int64_t ldx, int x_dtype, int8_t* q, int64_t ldq, float* s, int64_t M,
+                          int64_t K, fg_stream_t stream);
+
+int fg_quant_fp8_rowwise(const void* x, int64_t ldx, int x_dtype, uint8_t* q, int64_t ldq, float* s, int64_t M,
+                         int64_t K, const float* static_scale, const void* rms_weight, int rms_weight_dtype,
+                         float rms_eps, int32_t fuse_rmsnorm, fg_stream_t stream);
+
+/* FP8 quantisation with one scale per [block_m x block_k] tile of x: s[i, j] (row stride lds) covers rows
+ * i*block_m.. and columns j*block_k..; s = amax / 448 (1 if amax is not > 0) or *static_scale for every tile.
+ * block_m = 1, block_k = 128 is the reference's 1x128 activation blocks (gemm_fp8.py act_quant_blockwise),
+ * block_m = block_k = 128 its 128x128 weight blocks and block_m = M, block_k = K one per-tensor scale
+ * (oracle forge/kernels/ref/gemm_fp8.py:43-85, granularities block / block2d / per_tensor). */
+int fg_quant_fp8_block(const void* x, int64_t ldx, int x_dtype, uint8_t* q, int64_t ldq, float* s, int64_t lds,
+                       int64_t M, int64_t K, int32_t block_m, int32_t block_k, const float* static_scale,
+                       fg_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Library information.  fg_device_ok replaces the capability gate triton_usable (forge/kernels/ops_gemm.py:159-175):
+ * returns 1 when `device` is a gfx950 GPU this build can run on, else 0 (message in fg_last_error).
+ * ------------------------------------------------------------------------------------------------------------- */
+const char* fg_version(void);
+const char* fg_last_error(void);
+int fg_device_ok(int device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_MI355X_H */

@@ -1,0 +1,168 @@
+"""GPU parity of the W4A16 path (fg_w4a16_gemm / fg_w4_dequant through the C ABI) against the CPU oracle.
+
+Bars: dequantisation bit-exact; GEMM outputs within max|y - ref| / max|ref| <= 1e-2 of the fp32-accumulated oracle and
+inside the reference's compare() rule (rel 2e-3, abs 1e-3, rel_norm 2e-2, eps-aware for bf16/fp16 outputs).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from forge_amd import layouts as L
+from forge_amd import ops_gemm as ops
+from oracle import gemm as og
+from oracle import w4 as ow
+from tests._util import assert_close, gen, oracle_packed, to_f32, w4_parts, x_act
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ODT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
+
+
+def _case(m, n, k, gs, sym, xdt, *, bias=False, seed=0, impl=None, scale_dtype=torch.float16, xscale=1.0):
+    q, s, z = w4_parts(n, k, gs, sym, seed, scale_dtype)
+    p = L.pack_w4(q, s, z, gs).to(DEV)
+    x = x_act(m, k, xdt, seed + 1, xscale)
+    b = (torch.randn(n, generator=gen(seed + 2)) * 0.5).to(xdt) if bias else None
+    y = ops.w4a16_linear(x.to(DEV), p, None if b is None else b.to(DEV), config={"impl": impl} if impl else None)
+    assert ops.last_path("w4a16_linear") == "hip" and y.dtype == xdt and y.shape == (m, n)
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs), None if b is None else to_f32(b))
+    return y, ref
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (777, 2048)])
+@pytest.mark.parametrize("gs", [128, 32, -1])
+@pytest.mark.parametrize("sym", [False, True])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_gemv_decode_matches_oracle(m, n, k, gs, sym, xdt):
+    y, ref = _case(m, n, k, gs, sym, xdt, bias=(m % 2 == 1), seed=m + n, impl="gemv")
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"gemv m={m} n={n} k={k} gs={gs}")
+
+
+@pytest.mark.parametrize("m", [5, 16, 33, 64, 256])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (777, 2048)])
+@pytest.mark.parametrize("gs", [128, 32])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_mfma_matches_oracle(m, n, k, gs, xdt):
+    y, ref = _case(m, n, k, gs, sym=(m % 2 == 0), xdt=xdt, bias=True, seed=m, impl="mfma")
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"mfma m={m} n={n} k={k} gs={gs}")
+
+
+@pytest.mark.parametrize("m,n,k,gs", [(3, 333, 100, 32), (17, 129, 131, 8), (2, 64, 1001, 16), (40, 256, 256, -1)])
+def test_generic_kernel_odd_shapes(m, n, k, gs):
+    y, ref = _case(m, n, k, gs, False, torch.bfloat16, bias=True, seed=k)
+    assert_close(y.cpu(), ref, "bfloat16", what=f"auto m={m} n={n} k={k}")
+    y2, _ = _case(m, n, k, gs, False, torch.bfloat16, bias=True, seed=k, impl="generic")
+    assert_close(y2.cpu(), ref, "bfloat16", what="generic")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
+@pytest.mark.parametrize("gs", [128, 32])
+def test_act_order_regular_groups_use_sorted_fast_path(m, gs):
+    n, k = 1024, 2048
+    q, s, z = w4_parts(n, k, gs, False, seed=m)
+    g_idx = (torch.arange(k) // gs)[torch.randperm(k, generator=gen(9))].to(torch.int32)
+    p = L.pack_w4(q, s, z, gs, g_idx=g_idx).to(DEV)
+    pp = ops.prepare_w4(p)
+    assert L.cached_group_sort(pp, compute=False) not in (None, L.MISSING_SORT)
+    x = x_act(m, k, torch.bfloat16, seed=m + 1)
+    y = ops.w4a16_linear(x.to(DEV), p)
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs, g_idx))
+    assert_close(y.cpu(), ref, "bfloat16", what=f"act-order m={m}")
+
+
+def test_act_order_irregular_groups_use_generic_kernel():
+    n, k, gs = 300, 256, 64
+    q, s, z = w4_parts(n, k, gs, True, seed=3)
+    g_idx = torch.randint(0, 4, (k,), generator=gen(4), dtype=torch.int32)
+    p = L.pack_w4(q, s, z, gs, g_idx=g_idx).to(DEV)
+    x = x_act(5, k, torch.float16, seed=6)
+    y = ops.w4a16_linear(x.to(DEV), p)
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs, g_idx))
+    assert_close(y.cpu(), ref, "float16", what="irregular g_idx")
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("sym,gs", [(False, 128), (True, 32), (False, -1)])
+def test_dequant_is_bit_exact(scale_dtype, out, sym, gs):
+    n, k = 300, 1000
+    q, s, z = w4_parts(n, k, gs, sym, seed=7, scale_dtype=scale_dtype)
+    p = L.pack_w4(q, s, z, gs).to(DEV)
+    d = p.dequantize(out).cpu()
+    ref = ow.dequantize_parts(q.numpy(), s.float().numpy(), None if z is None else z.numpy(), gs)
+    if out == torch.float32:
+        assert np.array_equal(d.numpy(), ref)
+    else:
+        assert torch.equal(d, torch.from_numpy(ref).to(out))  # one rounding of the exact fp32 value
+
+
+@pytest.mark.parametrize("kn", [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)])
+@pytest.mark.parametrize("m", [1, 16])
+def test_llama3_8b_decode_shapes(kn, m):
+    """configs[1] shapes and distributions at full size."""
+    k, n = kn
+    y, ref = _case(m, n, k, 128, False, torch.bfloat16, seed=k + n)
+    assert_close(y.cpu(), ref, "bfloat16", what=f"llama K={k} N={n} M={m}")
+
+
+def test_impls_agree_and_runs_are_bit_reproducible():
+    q, s, z = w4_parts(2048, 4096, 128, False, seed=11)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(4, 4096, torch.bfloat16, seed=12).to(DEV)
+    outs = {impl: [ops.w4a16_linear(x, p, config={"impl": impl}) for _ in range(3)] for impl in ("gemv", "mfma", "generic")}
+    for impl, runs in outs.items():
+        assert all(torch.equal(runs[0], r) for r in runs[1:]), impl
+    ref = og.w4a16_gemm_ref(to_f32(x.cpu()), oracle_packed(q, s, z, 128))
+    for impl, runs in outs.items():
+        assert_close(runs[0].cpu(), ref, "bfloat16", what=impl)
+    # split-K MFMA path (M=16 on 2048 channels uses several K splits) is reproducible too
+    x16 = x_act(16, 4096, torch.bfloat16, seed=13).to(DEV)
+    r16 = [ops.w4a16_linear(x16, p) for _ in range(5)]
+    assert all(torch.equal(r16[0], r) for r in r16[1:])
+
+
+def test_edge_cases_nd_noncontiguous_empty_nan():
+    n, k, gs = 256, 512, 64
+    q, s, z = w4_parts(n, k, gs, True, seed=21)
+    p = L.pack_w4(q, s, z, gs).to(DEV)
+    op = oracle_packed(q, s, z, gs)
+    assert ops.w4a16_linear(torch.zeros(0, k, dtype=torch.bfloat16, device=DEV), p).shape == (0, n)
+    x3 = x_act(6, k, torch.bfloat16, seed=22).reshape(2, 3, k)
+    y3 = ops.w4a16_linear(x3.to(DEV), p)
+    assert y3.shape == (2, 3, n)
+    assert_close(y3.reshape(6, n).cpu(), og.w4a16_gemm_ref(to_f32(x3.reshape(6, k)), op), "bfloat16", what="n-d")
+    xt = x_act(2 * k, 3, torch.bfloat16, seed=23).t()  # [3, 2k] view with strides (1, 3)
+    ys = ops.w4a16_linear(xt.to(DEV)[:, :k], p)  # non-unit stride along K -> copied to rows by the op
+    assert_close(ys.cpu(), og.w4a16_gemm_ref(to_f32(xt[:, :k].contiguous()), op), "bfloat16", what="strided x")
+    xn = x_act(4, k, torch.float16, seed=24)
+    xn[1, 3] = float("nan")
+    xn[2, 5] = float("inf")
+    yn = ops.w4a16_linear(xn.to(DEV), p).cpu().float()
+    assert torch.isnan(yn[1]).all() and torch.isfinite(yn[0]).all() and torch.isfinite(yn[3]).all()
+    assert not torch.isfinite(yn[2]).all()
+
+
+def test_graph_capture_replays_match_eager():
+    q, s, z = w4_parts(4096, 4096, 128, False, seed=31)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    xs = [x_act(m, 4096, torch.bfloat16, seed=32 + m).to(DEV) for m in (1, 16)]
+    eager = [ops.w4a16_linear(x, p) for x in xs]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for x in xs:
+            ops.w4a16_linear(x, p)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [ops.w4a16_linear(x, p) for x in xs]
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        _ = ops.w4a16_linear(xs[0], p)  # eager work between replays
+        torch.cuda.synchronize()

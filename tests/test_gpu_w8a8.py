@@ -1,0 +1,147 @@
+"""GPU parity of the W8A8 path through the C ABI: INT8 GEMM (exact int32 accumulator, exact fp32 epilogue), FP8
+e4m3fn GEMM (all three scale modes), and the per-token / block quantisers, against the CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from forge_amd import ops_gemm as ops
+from oracle import gemm as og
+from tests._util import assert_close, fp8_codes, gen, to_f32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _int8_operands(m, n, k, seed):
+    x = torch.randn(m, k, generator=gen(seed)).numpy()
+    w = (torch.randn(n, k, generator=gen(seed + 1)) * 0.05).numpy()
+    xq, sx = og.quantize_int8_ref(x, "per_token")
+    wq, sw = og.quantize_int8_ref(w, "per_channel")
+    return xq, sx, wq, sw
+
+
+# ------------------------------------------------------------------------------------------------ INT8
+@pytest.mark.parametrize("m", [1, 16, 100, 513])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (777, 1000)])
+def test_int8_gemm_exact(m, n, k):
+    """int32 accumulator bit-exact; the fp32 epilogue equals the oracle bit for bit (torch.equal bar of
+    tests_gpu/test_kernels_gemm_fp8_int8.py:106-117)."""
+    xq, sx, wq, sw = _int8_operands(m, n, k, seed=m + n)
+    a, w = torch.from_numpy(xq).to(DEV), torch.from_numpy(wq).to(DEV)
+    acc = ops.int8_gemm(a, None, w, None, out_dtype=torch.int32).cpu().numpy()
+    ref_acc = og.int8_matmul_exact(xq, wq)
+    assert np.array_equal(acc, ref_acc)
+    b = torch.randn(n, generator=gen(7))
+    y = ops.int8_gemm(a, torch.from_numpy(sx).to(DEV), w, torch.from_numpy(sw).to(DEV), b.to(DEV),
+                      out_dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(y, og.int8_gemm_ref(xq, sx, wq, sw, b.numpy(), acc=ref_acc))
+
+
+@pytest.mark.parametrize("m", [0, 1, 16, 100])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_int8_linear_end_to_end(m, xdt):
+    n, k = 777, 1000
+    x = torch.randn(m, k, generator=gen(3)).to(xdt)
+    w = (torch.randn(n, k, generator=gen(4)) * 0.05)
+    wq, sw = og.quantize_int8_ref(w.numpy(), "per_channel")
+    y = ops.int8_linear(x.to(DEV), torch.from_numpy(wq).to(DEV), torch.from_numpy(sw).to(DEV))
+    assert ops.last_path("int8_linear") == "hip" and y.dtype == xdt and y.shape == (m, n)
+    if m == 0:
+        return
+    xr, sr = og.quantize_int8_ref(to_f32(x), "per_token")
+    assert_close(y.cpu(), og.int8_gemm_ref(xr, sr, wq, sw), "float16" if xdt == torch.float16 else "bfloat16")
+
+
+@pytest.mark.parametrize("m,k", [(1, 1000), (16, 4096), (100, 1000), (513, 4096)])
+def test_int8_quantiser_bit_exact(m, k):
+    x = torch.randn(m, k, generator=gen(m)).to(torch.float16)
+    q, s = ops.quantize_act_int8(x.to(DEV))
+    qr, sr = og.quantize_int8_ref(to_f32(x), "per_token")
+    assert np.array_equal(s.cpu().numpy(), sr)
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
+def test_int8_quantiser_ties_zero_rows_nan():
+    x = torch.tensor([[2.5, 127.0, -2.5, 0.5, 1.5, -126.5], [0.0] * 6, [1.0, float("nan"), 300.0, -3.0, 0.0, 2.0]])
+    q, s = ops.quantize_act_int8(x.to(DEV))
+    qr, sr = og.quantize_int8_ref(x.numpy(), "per_token")
+    assert np.array_equal(s.cpu().numpy(), sr) and np.array_equal(q.cpu().numpy(), qr)
+    assert q[0].tolist() == [2, 127, -2, 0, 2, -126]
+
+
+# ------------------------------------------------------------------------------------------------ FP8
+@pytest.mark.parametrize("gx,gw", [("per_tensor", "per_tensor"), ("per_token", "per_channel"), ("block", "block2d")])
+@pytest.mark.parametrize("m", [0, 1, 7, 64, 300])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1000, 2056), (256, 777)])
+def test_fp8_gemm_matches_oracle(gx, gw, m, n, k):
+    x = torch.randn(m, k, generator=gen(m + k)).to(torch.bfloat16)
+    w = torch.randn(n, k, generator=gen(n)) * 0.05
+    xq, sx = og.quantize_fp8_ref(to_f32(x), gx)
+    wq, sw = og.quantize_fp8_ref(w.numpy(), gw)
+    txq = torch.from_numpy(xq).view(torch.float8_e4m3fn).to(DEV)
+    twq = torch.from_numpy(wq).view(torch.float8_e4m3fn).to(DEV)
+    y = ops.fp8_linear(txq, twq, torch.from_numpy(sw).to(DEV), x_scale=torch.from_numpy(sx).to(DEV),
+                       out_dtype=torch.bfloat16)
+    assert ops.last_path("fp8_linear") == "hip" and y.shape == (m, n)
+    if m:
+        assert_close(y.cpu(), og.fp8_gemm_ref(xq, sx, wq, sw), "bfloat16", what=f"fp8 {gx}/{gw} m={m}")
+
+
+def test_fp8_gemm_is_bit_reproducible_and_bias():
+    x = torch.randn(256, 4096, generator=gen(1)).to(torch.bfloat16)
+    w = torch.randn(4096, 4096, generator=gen(2)) * 0.05
+    wq, sw = og.quantize_fp8_ref(w.numpy(), "per_channel")
+    twq, tsw = torch.from_numpy(wq).view(torch.float8_e4m3fn).to(DEV), torch.from_numpy(sw).to(DEV)
+    b = torch.randn(4096, generator=gen(3)).to(torch.bfloat16)
+    outs = [ops.fp8_linear(x.to(DEV), twq, tsw, b.to(DEV)) for _ in range(5)]
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    xq, sx = og.quantize_fp8_ref(to_f32(x), "per_token")
+    assert_close(outs[0].cpu(), og.fp8_gemm_ref(xq, sx, wq, sw, to_f32(b)), "bfloat16", what="fp8 e2e + bias")
+
+
+@pytest.mark.parametrize("gran,block", [("per_token", 128), ("per_tensor", 128), ("block", 128), ("block2d", 128),
+                                        ("block", 64)])
+@pytest.mark.parametrize("m,k", [(1, 64), (33, 1000), (300, 4096)])
+def test_fp8_quantiser_codes_bit_exact(gran, block, m, k):
+    x = (torch.randn(m, k, generator=gen(m * k)) * 3).to(torch.bfloat16)
+    x[0, : min(k, 5)] = torch.tensor([2 ** -12, -2 ** -10, 3 * 2 ** -11, 0.0, 1e-30])[: min(k, 5)].to(torch.bfloat16)
+    q, s = ops.quantize_act_fp8(x.to(DEV), granularity=gran, block=block)
+    qr, sr = og.quantize_fp8_ref(to_f32(x), gran, block=block)
+    assert np.array_equal(s.cpu().numpy().reshape(sr.shape), sr)
+    assert np.array_equal(fp8_codes(q), qr)
+
+
+def test_fp8_quantiser_edge_cases():
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    x[1] = 1e4
+    x[2, 0] = 1e-6
+    q, s = ops.quantize_act_fp8(x.to(DEV))
+    qr, sr = og.quantize_fp8_ref(to_f32(x), "per_token")
+    assert np.array_equal(fp8_codes(q), qr) and np.array_equal(s.cpu().numpy(), sr)
+    assert s[0].item() == 1.0 and q[1].float().abs().max().item() == 448.0
+    # static scale smaller than needed saturates (never NaN)
+    big = torch.tensor([[1000.0, -1000.0, 1.0]])
+    qs, _ = ops.quantize_act_fp8(big.to(DEV), granularity="per_tensor", scale=torch.tensor([1.0]))
+    assert qs.float().cpu().tolist() == [[448.0, -448.0, 1.0]]
+    xn = torch.randn(2, 128, generator=gen(5)).to(torch.bfloat16)
+    xn[0, 5] = float("nan")
+    qn, sn = ops.quantize_act_fp8(xn.to(DEV))
+    qnr, snr = og.quantize_fp8_ref(to_f32(xn), "per_token")
+    assert np.array_equal(sn.cpu().numpy(), snr)
+    assert np.array_equal(fp8_codes(qn)[1], qnr[1]) and torch.isfinite(qn[1].float()).all()
+
+
+@pytest.mark.parametrize("k", [64, 1000, 4096])
+def test_fused_rmsnorm_fp8_quantiser(k):
+    x = (torch.randn(33, k, generator=gen(k)) * 3).to(torch.bfloat16)
+    wt = (torch.rand(k, generator=gen(k + 1)) + 0.5).to(torch.bfloat16)
+    q, s = ops.quantize_act_fp8(x.to(DEV), rms_weight=wt.to(DEV), rms_eps=1e-6)
+    xf = to_f32(x).astype(np.float64)
+    y = (xf / np.sqrt((xf ** 2).mean(axis=-1, keepdims=True) + 1e-6) * to_f32(wt)).astype(np.float32)
+    qr, sr = og.quantize_fp8_ref(y, "per_token")
+    np.testing.assert_allclose(s.cpu().numpy(), sr, rtol=1e-5)
+    d, dr = og.dequantize_fp8_ref(fp8_codes(q), s.cpu().numpy()), og.dequantize_fp8_ref(qr, sr)
+    assert (np.abs(d - dr) <= np.abs(dr) * 0.07 + 1e-3 * sr.max()).all()
+    assert (fp8_codes(q) != qr).mean() < 0.01

@@ -1,0 +1,103 @@
+"""CPU tests of the product's packed formats (forge_amd.layouts) against the oracle's independent packer."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from forge_amd import layouts as L
+from forge_amd.errors import ConfigError, NotFound
+from oracle import w4 as ow
+from tests._util import w4_parts
+
+
+@pytest.mark.parametrize("n", [1, 7, 64, 65, 130])
+@pytest.mark.parametrize("k", [8, 33, 100, 257])
+@pytest.mark.parametrize("gs", [-1, 16, 64])
+@pytest.mark.parametrize("sym", [True, False])
+def test_product_pack_equals_oracle_pack(n, k, gs, sym):
+    q, s, z = w4_parts(n, k, gs, sym, seed=n * 7 + k)
+    p = L.pack_w4(q, s, z, gs)
+    o = ow.pack_w4(q.numpy(), s.numpy(), None if z is None else z.numpy(), gs)
+    assert np.array_equal(p.qweight.numpy(), o["qweight"])
+    assert np.array_equal(p.scales.numpy(), o["scales"])
+    assert (z is None and p.zeros is None) or np.array_equal(p.zeros.numpy(), o["zeros"])
+    q2, s2, z2 = L.unpack_w4(p)
+    assert torch.equal(q, q2) and torch.equal(s, s2) and ((z is None and z2 is None) or torch.equal(z, z2))
+    assert p.layout_id == ow.layout_id(4) == "w4.portable_row.v1-73e10e"
+
+
+@pytest.mark.parametrize("n,k,gs", [(33, 100, 32), (64, 128, 64), (7, 50, -1), (130, 257, 16)])
+def test_fragment_artifact_repacks_to_identical_portable_bytes(n, k, gs):
+    q, s, z = w4_parts(n, k, gs, False, seed=3)
+    a = L.pack_w4(q, s, z, gs, L.PORTABLE_W4)
+    b = L.repack(a, L.FRAGMENT_W4)
+    assert b.layout_id == "w4.mma_fragment_k16n64.v1-445296"
+    assert b.qweight.shape == ((k + 15) // 16, ((n + 63) // 64) * 128)
+    for x, y in zip(L.unpack_w4(a), L.unpack_w4(b)):
+        assert (x is None and y is None) or torch.equal(x, y)
+    back = L.repack(b, L.PORTABLE_W4)
+    assert torch.equal(back.qweight, a.qweight) and torch.equal(back.scales, a.scales) and torch.equal(back.zeros, a.zeros)
+    assert L.repack(a, L.PORTABLE_W4) is a
+
+
+def test_fragment_permutation_lane_ownership():
+    """Lane l owns k = 2(l%4)+{0,1}(+8), n = 8 nb + l//4 (tests/test_kernels_gemm_layouts.py:185-195)."""
+    idx, inv = L.fragment_tile_perm((0, 1, 2, 3, 4, 5, 6, 7))
+    assert sorted(idx.tolist()) == list(range(1024)) and torch.equal(inv[idx], torch.arange(1024))
+    lane = 5
+    mine = idx[lane * 32:(lane + 1) * 32]
+    ks, ns = mine // 64, mine % 64
+    assert set((ns % 8).tolist()) == {lane // 4}
+    assert ks.tolist()[:4] == [2 * (lane % 4), 2 * (lane % 4) + 1, 2 * (lane % 4) + 8, 2 * (lane % 4) + 9]
+
+
+def test_packer_validation_errors():
+    q, s, z = w4_parts(8, 32, 16, True)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q + 16, s, z, 16)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q, s[:, :1], z, 16)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q, s, z, 12)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q.float(), s, z, 16)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q, s, z, 8, L.FRAGMENT_W4)
+    with pytest.raises(ConfigError):
+        L.pack_w4(q, s, z, 16, L.PORTABLE_W8)
+    with pytest.raises(NotFound):
+        L.get_layout("nope")
+
+
+def test_state_roundtrip_and_size():
+    q, s, z = w4_parts(64, 256, 128, False)
+    p = L.pack_w4(q, s, z, 128)
+    p2 = L.PackedW4.from_tensors(p.tensors(), p.state())
+    assert p2.layout_id == p.layout_id and torch.equal(p2.qweight, p.qweight)
+    assert abs(p.bits_per_weight - (4 + 20 / 128)) < 0.2
+    assert L.PackedW4.tensor_roles()["qweight"] == "payload"
+
+
+def test_act_order_sort_matches_oracle():
+    n, k, gs = 24, 96, 32
+    q, s, _ = w4_parts(n, k, gs, True, seed=4)
+    g = torch.Generator().manual_seed(5)
+    g_idx = (torch.arange(k) // gs)[torch.randperm(k, generator=g)].to(torch.int32)
+    p = L.pack_w4(q, s, None, gs, g_idx=g_idx)
+    sp, perm = L.sort_columns_by_group(p)
+    osp, operm = ow.sort_columns_by_group(ow.pack_w4(q.numpy(), s.numpy(), None, gs, g_idx.numpy()))
+    assert np.array_equal(perm.numpy(), operm) and np.array_equal(sp.qweight.numpy(), osp["qweight"])
+    assert L.cached_group_sort(p)[1] is L.cached_group_sort(p)[1]  # cached
+    assert L.cached_group_sort(L.pack_w4(q, s, None, gs)) is None
+
+
+def test_rtn_quantiser_bounds():
+    w = torch.randn(16, 100, generator=torch.Generator().manual_seed(0))
+    for sym in (True, False):
+        q, s, z = L.quantize_w4_rtn(w, 32, sym=sym, scale_dtype=torch.float32)
+        gi = torch.arange(100) // 32
+        zz = 8.0 if z is None else z.float()[:, gi]
+        deq = (q.float() - zz) * s[:, gi]
+        assert q.max() <= 15 and (z is None) == sym
+        assert (deq - w).abs().max() <= s.max() * 0.51 + 1e-6
