@@ -27,6 +27,12 @@ hipError_t launch_w4_mfma(const void* x, int64_t ldx, bool xbf16, const int32_t*
                           int tile_m, int splits, hipStream_t s);
 void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchunk, int* used);
 size_t w4_gemv_lds_bytes(int mt, int K);
+hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                               const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                               const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                               int K, int gs, int G, int tile_n, hipStream_t s);
+bool w4_gemv_tile_ok(int mt, int N, int K, int G, int tile_n);
+size_t w4_gemv_tile_lds_bytes(int mt, int K, int G, int TN);
 hipError_t launch_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
                             int64_t ldy, int ydt, int M, int N, int K, int tile, hipStream_t s);
@@ -109,8 +115,11 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
             const fg_w4_config* cfg, W4Plan* p) {
   const int gs = group_size > 0 ? group_size : (int)K;
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
+  const int G = (int)((K + gs - 1) / gs);
+  const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  const bool tile_fits = fg::w4_gemv_tile_ok(mt, (int)N, (int)K, G, cfg ? cfg->tile_n : 0);
   const bool gemv_ok = !has_g_idx && q_aligned && (gs % 32 == 0 || group_size <= 0) && M <= 4 &&
-                       fg::w4_gemv_lds_bytes(4, (int)K) <= 150 * 1024;
+                       (tile_fits || fg::w4_gemv_lds_bytes(4, (int)K) <= 150 * 1024);
   const bool mfma_ok = !has_g_idx && q_aligned && x_aligned && (K % 8 == 0);
   int use = impl;
   if (use == FG_W4_AUTO) use = gemv_ok ? FG_W4_GEMV : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC);
@@ -183,7 +192,11 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
-  if (p.impl == FG_W4_GEMV) {
+  const bool tile_fits = fg::w4_gemv_tile_ok(p.mt, (int)N, (int)K, (int)G, cfg ? cfg->tile_n : 0);
+  if (p.impl == FG_W4_GEMV && tile_fits && !(cfg && cfg->rows_per_wave)) {
+    e = fg::launch_w4_gemv_tile(p.mt, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
+                                bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, (int)G, cfg ? cfg->tile_n : 0, s);
+  } else if (p.impl == FG_W4_GEMV) {
     e = fg::launch_w4_gemv(p.mt, p.rows, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
                            bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, p.max_blocks, s);
   } else if (p.impl == FG_W4_MFMA) {

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/forge_mi355x.h"
 
 namespace fg {
@@ -18,6 +20,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
   u += 0x7fffu + ((u >> 16) & 1u);                                            // round half to even
   return (uint16_t)(u >> 16);
+}
+
+// Hardware conversion (v_cvt_pk_bf16_f32): round to nearest even, NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits_hw(float f) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+  const bf16x2v_t h = __builtin_convertvector((f32x2_t){f, f}, bf16x2v_t);
+  return (uint16_t)__builtin_bit_cast(uint32_t, h);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
@@ -60,6 +70,79 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
   return v;
+}
+
+// Quotient n / d for n * d < 2^32 with one multiply-high (d == 1 passes n through): m = floor((2^32 - 1) / d) + 1 is
+// floor(2^32 / d) + 1 (or 2^32 / d for powers of two), and n * m / 2^32 = n / d + n * e / 2^32 with 0 <= e <= 1 never
+// carries past the next integer while n * d < 2^32.
+struct FastDiv {
+  uint32_t d, m;
+  __device__ __forceinline__ explicit FastDiv(uint32_t d_) : d(d_), m(d_ > 1 ? 0xffffffffu / d_ + 1u : 0u) {}
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return d > 1 ? __umulhi(n, m) : n; }
+};
+
+// Value of lane l ^ o (o = 1, 2) or of a partner in the other o-half of its 8/16-lane group (o = 4: mirror within 8
+// lanes, o = 8: rotate by 8 within 16 lanes) through DPP, without LDS traffic.
+template <int O>
+__device__ __forceinline__ float dpp_partner(float v) {
+  constexpr int ctrl = O == 1 ? 0xB1 : (O == 2 ? 0x4E : (O == 4 ? 0x141 : 0x128));
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+}
+
+// In-place v_permlane32_swap_b32 / v_permlane16_swap_b32: a's lanes 32-63 trade places with b's lanes 0-31 (32), or
+// a's odd 16-lane rows with b's even rows (16).  Written as asm because this compiler folds the builtin's second
+// result into its first when both feed one add.  s_nop 1 gives the two wait states a VALU write needs before a
+// permlane swap reads it (and the same after, for the consumer).
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Sum each of V (4, 8 or 16) values over the 64 lanes; every lane of the group of 64/V lanes that starts at
+// (l / (64/V)) * (64/V) ends with the same total of value l / (64/V).  Halving steps exchange half of the live values
+// with the partner half of the wave: across 32 lanes with v_permlane32_swap, across 16 with v_permlane16_swap, then
+// within 16-lane rows through DPP, so V values cost V-1 exchanges plus the log2 of the final group size.
+template <int V>
+__device__ __forceinline__ float wave_transpose_sum(float (&v)[V], int lane) {
+  static_assert(V == 4 || V == 8 || V == 16, "V");
+  float cur[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) cur[i] = v[i];
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) {  // lanes 0-31 keep values [0, V/2), lanes 32-63 keep [V/2, V)
+    float a = cur[i], b = cur[i + V / 2];
+    permlane32_swap(a, b);  // a = [cur_i lanes 0-31, cur_j lanes 0-31], b = [cur_i lanes 32-63, cur_j lanes 32-63]
+    cur[i] = a + b;
+  }
+#pragma unroll
+  for (int i = 0; i < V / 4; ++i) {  // even 16-lane rows keep the lower quarter, odd rows the upper one
+    float a = cur[i], b = cur[i + V / 4];
+    permlane16_swap(a, b);
+    cur[i] = a + b;
+  }
+  auto step = [&](auto o_tag, int n) {
+    constexpr int O = decltype(o_tag)::value;
+    const bool up = (lane & O) != 0;
+    if (n > 1) {
+#pragma unroll
+      for (int i = 0; i < V / 8; ++i) {
+        if (i < n / 2) {
+          const float send = up ? cur[i] : cur[i + n / 2];
+          const float keep = up ? cur[i + n / 2] : cur[i];
+          cur[i] = keep + dpp_partner<O>(send);
+        }
+      }
+    } else {
+      cur[0] += dpp_partner<O>(cur[0]);
+    }
+  };
+  step(std::integral_constant<int, 8>{}, V / 4);
+  step(std::integral_constant<int, 4>{}, V / 8 > 0 ? V / 8 : 1);
+  step(std::integral_constant<int, 2>{}, V / 16 > 0 ? V / 16 : 1);
+  step(std::integral_constant<int, 1>{}, 1);
+  return cur[0];
 }
 
 // Map a linear workgroup id to an output tile: first deal consecutive logical tiles to one XCD, then walk tiles in

@@ -178,6 +178,311 @@ __global__ void __launch_bounds__(256) w4_gemv_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------------ GEMV (tiled)
+constexpr int kTileMaxWaves = 12;  // wavefronts per workgroup of the tiled GEMV (three per SIMD)
+
+constexpr int kStageU = 8;         // items per thread and pass of the tile staging
+
+// Wavefront cap of a tiled-GEMV variant, from its register need (fetch buffers grow with the chunks per lane S, x
+// pairs and accumulators with the rows of x MT): three waves per SIMD leave 168 VGPRs, two leave 256, one 512.
+__host__ __device__ constexpr int w4_tile_max_waves(int mt, int s) {
+  return mt == 1 ? (s <= 2 ? kTileMaxWaves : 8) : (mt == 2 ? (s <= 6 ? 8 : 4) : (s <= 3 ? 8 : 4));
+}
+
+// Sum of a value over the four lanes of an aligned quad (row-local DPP, no LDS traffic).  Every lane of the quad gets
+// the same total, (v0 + v1) + (v2 + v3) in one order.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  return v;
+}
+
+__device__ __forceinline__ float raw_bits_to_f32(uint32_t raw, int dt) {
+  return dt == FG_F32 ? __builtin_bit_cast(float, raw)
+                      : (dt == FG_BF16 ? bf16_bits_to_f32(raw) : f16_bits_to_f32((uint16_t)raw));
+}
+
+// Element i of a 16- or 32-bit float array as raw bits (converted after the wait by raw_bits_to_f32).
+__device__ __forceinline__ uint32_t load_raw(const void* p, int dt, int64_t i) {
+  return dt == FG_F32 ? static_cast<const uint32_t*>(p)[i] : (uint32_t) static_cast<const uint16_t*>(p)[i];
+}
+
+// Stage everything a tile of TN channels [tile0, tile0+TN) reads besides qweight into LDS:
+//   xq[(m*4 + i) * KC + c] = word 4c+i of x row m as 16-bit pairs (x0,x2) (x1,x3) (x4,x6) (x5,x7), the order in
+//                            which the byte-permute unpack produces nibble pairs;  xs[m*KC + c] = fp32 sum of chunk c;
+//   ssc[g*TN + r] = fp32 scale of channel tile0+r in group g;  szb[g*TN + r] = fp32 (B + zero-point);
+//   sbias[r] = fp32 bias (0 without bias).
+// Each pass first issues every global load it needs (up to kStageU x words and kStageU scales per thread, one zero
+// word and one bias value), then converts and stores, so a pass costs one memory round trip; decode shapes need a
+// single pass.  Item indices are split with multiply-high division.
+template <int MT, bool XBF16>
+__device__ __forceinline__ void stage_tile(const uint16_t* __restrict__ x, int64_t ldx,
+                                           const int32_t* __restrict__ perm, const void* __restrict__ scales, int sdt,
+                                           int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz,
+                                           const void* __restrict__ bias, int bdt, int M, int N, int K, int KW, int KC,
+                                           int G, int TN, int tile0, int nthr, uint4* xq, float* xs, float* ssc,
+                                           float* szb, float* sbias) {
+  constexpr float kBias = XBF16 ? 128.f : 1024.f;
+  const int tid = threadIdx.x;
+  const int nw = 4 * KC;       // x words per row, padded to whole chunks
+  const int nx = MT * nw;      // item u = m * nw + w
+  const int ns = G * TN;
+  const int zpr = TN / 8;      // zero words per group row of the tile (tile0 and TN are multiples of 8)
+  const int nz = G * zpr;
+  const FastDiv div_w(nw), div_tn(TN), div_z(zpr);
+  const int per = kStageU * nthr;
+  const int passes = max(max((nx + per - 1) / per, (ns + per - 1) / per),
+                         max((nz + nthr - 1) / nthr, (TN + nthr - 1) / nthr));
+  const bool vec = perm == nullptr && (K & 7) == 0 && (ldx & 7) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  for (int p = 0; p < passes; ++p) {
+    uint4 xr[kStageU];
+    uint32_t sr[kStageU];
+#pragma unroll
+    for (int j = 0; j < kStageU; ++j) {
+      const int u = (p * kStageU + j) * nthr + tid;
+      const int m = (int)div_w.div((uint32_t)u), w = u - m * nw;
+      xr[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (u < nx && m < M && w < KW) {
+        const uint16_t* xrow = x + (int64_t)m * ldx;
+        if (vec) {
+          xr[j] = reinterpret_cast<const uint4*>(xrow)[w];
+        } else {
+          uint32_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int k = 8 * w + e;
+            h[e] = k < K ? xrow[perm ? perm[k] : k] : 0u;
+          }
+          xr[j] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        }
+      }
+    }
+    // one dtype branch around the whole batch keeps the scale loads back to back
+    if (sdt == FG_F32) {
+#pragma unroll
+      for (int j = 0; j < kStageU; ++j) {
+        const int t = (p * kStageU + j) * nthr + tid;
+        const int g = (int)div_tn.div((uint32_t)t), r = t - g * TN;
+        if (t < ns) sr[j] = static_cast<const uint32_t*>(scales)[(int64_t)g * lds + min(tile0 + r, N - 1)];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kStageU; ++j) {
+        const int t = (p * kStageU + j) * nthr + tid;
+        const int g = (int)div_tn.div((uint32_t)t), r = t - g * TN;
+        if (t < ns) sr[j] = static_cast<const uint16_t*>(scales)[(int64_t)g * lds + min(tile0 + r, N - 1)];
+      }
+    }
+    const int tz = p * nthr + tid;
+    const int gz = (int)div_z.div((uint32_t)tz), vz = tz - gz * zpr;
+    uint32_t zr = 0x88888888u;
+    if (zeros && tz < nz) zr = (uint32_t)zeros[(int64_t)gz * ldz + min(tile0 / 8 + vz, (N - 1) / 8)];
+    uint32_t br = 0u;
+    if (bias && tz < TN) br = load_raw(bias, bdt, min(tile0 + tz, N - 1));
+
+    // ---- convert and store
+#pragma unroll
+    for (int j = 0; j < kStageU; ++j) {
+      const int u = (p * kStageU + j) * nthr + tid;
+      if (u < nx) {  // whole quads: nx and the quad's first item are multiples of 4
+        const int m = (int)div_w.div((uint32_t)u), w = u - m * nw;
+        const uint32_t e4[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+        uint32_t h[8];
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[2 * e] = e4[e] & 0xffffu;
+          h[2 * e + 1] = e4[e] >> 16;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += x_to_f32<XBF16>(h[e]);
+        sum = quad_sum(sum);  // the four words of a chunk sit in four consecutive lanes
+        const int c = w >> 2, i = w & 3;
+        xq[(m * 4 + i) * KC + c] = make_uint4(h[0] | (h[2] << 16), h[1] | (h[3] << 16), h[4] | (h[6] << 16),
+                                              h[5] | (h[7] << 16));
+        if (i == 0) xs[m * KC + c] = sum;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kStageU; ++j) {
+      const int t = (p * kStageU + j) * nthr + tid;
+      if (t < ns) ssc[t] = raw_bits_to_f32(sr[j], sdt);
+    }
+    if (tz < nz) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) szb[gz * TN + 8 * vz + e] = kBias + (float)nibble(zr, e);
+    }
+    if (tz < TN) sbias[tz] = raw_bits_to_f32(br, bias ? bdt : FG_F32);
+  }
+}
+
+// LDS bytes of the tiled GEMV: x pair units + chunk sums, then per-tile fp32 scales and fp32 (B + zero) [G][TN],
+// then the tile's fp32 bias [TN].
+__host__ __device__ inline size_t w4_gemv_tile_scale_offset(int mt, int KC) {
+  return ((size_t)mt * KC * (4 * 16 + 4) + 15) / 16 * 16;  // 16-byte aligned for float4 reads
+}
+
+size_t w4_gemv_tile_lds_bytes(int mt, int K, int G, int TN) {
+  const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
+  return w4_gemv_tile_scale_offset(mt, KC) + (size_t)G * TN * 8 + (size_t)TN * 4;
+}
+
+struct W4TilePlan {
+  int s;       // 16-byte chunks per lane and channel
+  int tn;      // channels per workgroup tile
+  int waves;   // wavefronts per workgroup
+  size_t lds;  // dynamic LDS bytes
+};
+
+// y[M,N] = x[M,K] @ dequant(W)^T (+bias) for M <= MT, K <= 2048*S, group size a multiple of 32 (or one group).
+// Workgroup = one tile of TN consecutive output channels (TN a multiple of 8, sized by the host so that the tiles
+// spread evenly over the CUs, one workgroup each); its `waves` wavefronts take the tile's 4-channel row blocks
+// round-robin.  The tile's x, scales, zero-points and bias are staged into LDS in one memory round trip (the [G, N]
+// scale layout otherwise costs one cache line per group per block), converted once to fp32 scale and fp32 (B + zero).
+// A block's S chunk loads per channel are issued together; the first block's loads go out before the staging, and
+// for S <= 2 the next block is fetched while the current one is computed.  Nibble pairs (q0,q2) (q1,q3) (q4,q6) (q5,q7) of a word come from two masks and
+// four byte-permutes against the magic exponent byte (bf16 0x43: 128+q, fp16 0x64: 1024+q).
+// Requires ldq % 4 == 0 and a 16-byte aligned qweight.
+template <int MT, int S, bool XBF16>
+__global__ void __launch_bounds__(w4_tile_max_waves(MT, S) * kWave) w4_gemv_tile_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ qw, int64_t ldq,
+    const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz,
+    const int32_t* __restrict__ perm, const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy,
+    int M, int N, int K, int gs, int G, int TN, int waves) {
+  constexpr int R = 4;
+  constexpr bool PF = S <= 2;
+  constexpr uint32_t kMagicBytes = XBF16 ? 0x43434343u : 0x64646464u;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int KW = (K + 7) / 8;
+  const int KC = (KW + 3) / 4;
+  uint4* xq = reinterpret_cast<uint4*>(smem);
+  float* xs = reinterpret_cast<float*>(smem + (size_t)MT * 4 * KC * 16);
+  float* ssc = reinterpret_cast<float*>(smem + w4_gemv_tile_scale_offset(MT, KC));
+  float* szb = ssc + (size_t)G * TN;
+  float* sbias = szb + (size_t)G * TN;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  // Wave-uniform (scalar) block index: the block loop then branches on scalars and row addresses are scalar math.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int tile0 = blockIdx.x * TN;
+  const int rows = min(TN, N - tile0);
+  const int nblk = (rows + R - 1) / R;
+  const int64_t ldq4 = ldq / 4;
+  const uint4* __restrict__ qw4 = reinterpret_cast<const uint4*>(qw);
+  const bool full = (KC % kWave) == 0 && KC == S * kWave;  // every chunk slot of every lane is real
+
+  // Branch-free fetch of one 4-channel block: rows past N re-read row N-1 and chunk slots past KC re-read chunk KC-1
+  // (their products are skipped), so every lane issues the same straight-line run of 16-byte loads.
+  int cl[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) cl[i] = min(lane + kWave * i, KC - 1);
+  auto fetch = [&](int blk, uint4 (&w)[R][S]) {
+    const int n0 = tile0 + blk * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint4* rp = qw4 + (int64_t)min(n0 + r, N - 1) * ldq4;
+#pragma unroll
+      for (int i = 0; i < S; ++i) w[r][i] = load16_stream(rp + cl[i]);
+    }
+  };
+
+  uint4 wa[R][S], wb[R][S];
+  int blk = wave;
+  fetch(min(blk, nblk - 1), wa);  // weight bytes are in flight while x, scales and zeros are staged
+
+  stage_tile<MT, XBF16>(x, ldx, perm, scales, sdt, lds, zeros, ldz, bias, bdt, M, N, K, KW, KC, G, TN, tile0,
+                        waves * kWave, xq, xs, ssc, szb, sbias);
+  __syncthreads();
+
+  auto compute = [&](int blk, const uint4 (&w)[R][S]) {
+    const int r0 = blk * R;
+    float acc[R * MT];
+#pragma unroll
+    for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int c = lane + kWave * i;
+      if (!full && c >= KC) continue;
+      const int g = (32 * c) / gs;
+      const float4 sc4 = *reinterpret_cast<const float4*>(ssc + g * TN + r0);
+      const float4 zb4 = *reinterpret_cast<const float4*>(szb + g * TN + r0);
+      const float sc[R] = {sc4.x, sc4.y, sc4.z, sc4.w};
+      const float zb[R] = {zb4.x, zb4.y, zb4.z, zb4.w};
+      uint4 xu[MT][4];
+      float xsum[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xu[m][q] = xq[(m * 4 + q) * KC + c];
+        xsum[m] = xs[m * KC + c];
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) d[m] = -zb[r] * xsum[m];
+        const uint32_t wq[4] = {w[r][i].x, w[r][i].y, w[r][i].z, w[r][i].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // nibble pairs (q0,q2) (q1,q3) (q4,q6) (q5,q7) as exact 16-bit floats B + q
+          const uint32_t lo = wq[q] & 0x0F0F0F0Fu, hi = (wq[q] >> 4) & 0x0F0F0F0Fu;
+          const uint32_t p0 = __builtin_amdgcn_perm(kMagicBytes, lo, 0x04010400u);
+          const uint32_t p1 = __builtin_amdgcn_perm(kMagicBytes, hi, 0x04010400u);
+          const uint32_t p2 = __builtin_amdgcn_perm(kMagicBytes, lo, 0x04030402u);
+          const uint32_t p3 = __builtin_amdgcn_perm(kMagicBytes, hi, 0x04030402u);
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            d[m] = dot2_acc<XBF16>(xu[m][q].x, p0, d[m]);
+            d[m] = dot2_acc<XBF16>(xu[m][q].y, p1, d[m]);
+            d[m] = dot2_acc<XBF16>(xu[m][q].z, p2, d[m]);
+            d[m] = dot2_acc<XBF16>(xu[m][q].w, p3, d[m]);
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r * MT + m] = __builtin_fmaf(sc[r], d[m], acc[r * MT + m]);
+      }
+    }
+    const float tot = wave_transpose_sum<R * MT>(acc, lane);
+    constexpr int span = kWave / (R * MT);
+    if ((lane % span) == 0) {
+      const int idx = lane / span;
+      const int r = idx / MT, m = idx - (idx / MT) * MT;
+      const int n = tile0 + r0 + r;
+      if (r0 + r < rows && m < M) {
+        const float v = tot + sbias[r0 + r];
+        y[(int64_t)m * ldy + n] = XBF16 ? f32_to_bf16_bits_hw(v) : f32_to_f16_bits(v);
+      }
+    }
+  };
+
+  const int cnt = blk < nblk ? (nblk - 1 - blk) / waves + 1 : 0;  // blocks of this wave: blk, blk + waves, ...
+  if constexpr (PF) {
+    // Counted loop over pairs while at least three blocks remain, then a peeled tail of one or two blocks: every
+    // path into the loop header has only buffer A in flight, so compute on one buffer waits only for its own loads
+    // while the other buffer's loads stay in flight, and no block is fetched without being used.
+    int left = cnt;
+    for (; left > 2; left -= 2) {
+      fetch(blk + waves, wb);
+      compute(blk, wa);
+      fetch(blk + 2 * waves, wa);
+      compute(blk + waves, wb);
+      blk += 2 * waves;
+    }
+    if (left == 2) {
+      fetch(blk + waves, wb);
+      compute(blk, wa);
+      compute(blk + waves, wb);
+    } else if (left == 1) {
+      compute(blk, wa);
+    }
+  } else {
+    for (int i = 0; i < cnt; ++i, blk += waves) {
+      if (i) fetch(blk, wa);
+      compute(blk, wa);
+    }
+  }
+}
+
 // Generic kernel: any group size (multiple of 8), per-column g_idx, any ldq / alignment, any M.
 // One wavefront per (output channel n, block of 4 rows of x); each weight element is dequantised exactly as the
 // oracle does ((q - z) * s in fp32) and accumulated in fp32.
@@ -290,6 +595,103 @@ hipError_t launch_w4_gemv(int mt, int R, bool xbf16, const void* x, int64_t ldx,
     FG_GEMV(4, false);
   }
 #undef FG_GEMV
+}
+
+static int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+template <int MT, int S, bool XBF16>
+static hipError_t launch_gemv_tile_t(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales,
+                                     int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                                     const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
+                                     int G, const W4TilePlan& tp, hipStream_t s) {
+  auto kern = w4_gemv_tile_kernel<MT, S, XBF16>;
+  if (tp.lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)tp.lds);
+    if (e != hipSuccess) return e;
+  }
+  const int blocks = (N + tp.tn - 1) / tp.tn;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(tp.waves * kWave), tp.lds, s, static_cast<const uint16_t*>(x), ldx, qw,
+                     ldq, scales, sdt, lds, zeros, ldz, perm, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gs, G,
+                     tp.tn, tp.waves);
+  return hipGetLastError();
+}
+
+template <int MT, bool XBF16>
+static hipError_t launch_gemv_tile_s(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales,
+                                     int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                                     const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
+                                     int G, const W4TilePlan& tp, hipStream_t s) {
+#define FG_GT(S_) \
+  return launch_gemv_tile_t<MT, S_, XBF16>(x, ldx, qw, ldq, scales, sdt, lds, zeros, ldz, perm, bias, bdt, y, ldy, M, N, K, gs, G, tp, s)
+  switch (tp.s) {
+    case 1: FG_GT(1);
+    case 2: FG_GT(2);
+    case 3: FG_GT(3);
+    case 4: FG_GT(4);
+    case 5: FG_GT(5);
+    case 6: FG_GT(6);
+    case 7: FG_GT(7);
+    default: FG_GT(8);
+  }
+#undef FG_GT
+}
+
+// Launch shape of the tiled GEMV.  Tiles: TN = 8 * ceil(N / (8 * CUs)) channels (or the caller's tile_n, rounded up
+// to a multiple of 8), halved while the tile's LDS exceeds 160 KiB.  Wavefronts: the tile's ceil(TN/4) row blocks are
+// shared evenly when a divisor in [4, cap] exists (the largest one), else min(blocks, cap), cap = w4_tile_max_waves.  Returns false when K is
+// beyond the kernel's reach (more than 8 chunks per lane) or nothing fits in LDS.
+bool w4_gemv_tile_plan(int mt, int N, int K, int G, int tile_n, W4TilePlan* tp) {
+  const int KC = ((K + 7) / 8 + 3) / 4;
+  const int S = (KC + 63) / 64;
+  if (S > 8 || N <= 0) return false;
+  int tn = tile_n > 0 ? (tile_n + 7) / 8 * 8 : 8 * ((N + 8 * device_cus() - 1) / (8 * device_cus()));
+  tn = max(tn, 8);
+  while (w4_gemv_tile_lds_bytes(mt, K, G, tn) > 160 * 1024 && tn > 8) tn = max(8, (tn / 2 + 7) / 8 * 8);
+  const size_t shm = w4_gemv_tile_lds_bytes(mt, K, G, tn);
+  if (shm > 160 * 1024) return false;
+  const int nb = (tn + 3) / 4;
+  const int cap = w4_tile_max_waves(mt, S);
+  int waves = min(nb, cap);
+  if (nb > cap) {
+    for (int w = cap; w >= 4; --w)
+      if (nb % w == 0) { waves = w; break; }
+  }
+  *tp = W4TilePlan{S, tn, waves, shm};
+  return true;
+}
+
+bool w4_gemv_tile_ok(int mt, int N, int K, int G, int tile_n) {
+  W4TilePlan tp;
+  return w4_gemv_tile_plan(mt, N, K, G, tile_n, &tp);
+}
+
+hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                               const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                               const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                               int K, int gs, int G, int tile_n, hipStream_t s) {
+  W4TilePlan tp;
+  if (!w4_gemv_tile_plan(mt, N, K, G, tile_n, &tp)) return hipErrorInvalidValue;
+#define FG_GTM(MT_, XB_) \
+  return launch_gemv_tile_s<MT_, XB_>(x, ldx, qw, ldq, scales, sdt, lds, zeros, ldz, perm, bias, bdt, y, ldy, M, N, K, gs, G, tp, s)
+  if (xbf16) {
+    if (mt == 1) FG_GTM(1, true);
+    if (mt == 2) FG_GTM(2, true);
+    FG_GTM(4, true);
+  } else {
+    if (mt == 1) FG_GTM(1, false);
+    if (mt == 2) FG_GTM(2, false);
+    FG_GTM(4, false);
+  }
+#undef FG_GTM
 }
 
 hipError_t launch_w4_generic(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,

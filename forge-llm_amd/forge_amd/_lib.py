@@ -43,7 +43,8 @@ class KernelLaunchError(ForgeError):
 
 class W4Config(ctypes.Structure):
     _fields_ = [("impl", ctypes.c_int32), ("rows_per_wave", ctypes.c_int32), ("max_blocks", ctypes.c_int32),
-                ("tile_m", ctypes.c_int32), ("split_k", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
+                ("tile_m", ctypes.c_int32), ("split_k", ctypes.c_int32), ("tile_n", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 2)]
 
 
 class MMConfig(ctypes.Structure):

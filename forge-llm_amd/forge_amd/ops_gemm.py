@@ -151,7 +151,7 @@ def _w4_config(config: dict[str, Any] | None) -> _lib.W4Config | None:
     if c.get("impl") not in _IMPL_ALIASES:
         raise ConfigError(f"unknown W4A16 impl {c.get('impl')!r}; choose gemv, mfma or generic")
     return _lib.W4Config(_lib.W4_IMPL[impl], int(c.get("rows_per_wave") or 0), int(c.get("max_blocks") or 0),
-                         int(c.get("tile_m") or 0), int(c.get("split_k") or 0))
+                         int(c.get("tile_m") or 0), int(c.get("split_k") or 0), int(c.get("tile_n") or 0))
 
 
 def _w4_launch(x2: torch.Tensor, p: PackedW4, perm: torch.Tensor | None, g_idx: torch.Tensor | None,

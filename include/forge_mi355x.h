@@ -43,7 +43,8 @@ typedef struct fg_w4_config {
   int32_t max_blocks;   /* GEMV: cap on workgroups (grid-stride beyond it) */
   int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128) */
   int32_t split_k;      /* MFMA: K splits (fp32 partials in the workspace, reduced in fixed order) */
-  int32_t reserved[3];
+  int32_t tile_n;       /* GEMV: output channels per workgroup tile (rounded up to a multiple of 8; 0 = policy) */
+  int32_t reserved[2];
 } fg_w4_config;
 
 typedef struct fg_mm_config {

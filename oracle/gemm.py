@@ -139,6 +139,20 @@ def quantize_fp8_ref(x: np.ndarray, granularity: str = "per_token", *, block: in
     return e4m3_encode(v), np.ascontiguousarray(s.astype(np.float32))
 
 
+def rmsnorm_act_quant_fp8_ref(x: np.ndarray, weight: np.ndarray | None, eps: float = 1e-6, *,
+                              granularity: str = "per_token", block: int = 128) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Fused producer oracle (``forge/kernels/ref/gemm_fp8.py:130-150``): ``y = x * rsqrt(mean(x^2) + eps) * w`` in fp32
+    (rsqrt = 1 / sqrt, each correctly rounded), then FP8 quantisation of ``y``.  Returns ``(codes, scale, y)``."""
+    xf = np.asarray(x, dtype=np.float32)
+    ms = (xf * xf).mean(axis=-1, keepdims=True, dtype=np.float32)
+    r = (np.float32(1.0) / np.sqrt((ms + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    y = (xf * r).astype(np.float32)
+    if weight is not None:
+        y = (y * np.asarray(weight, dtype=np.float32)).astype(np.float32)
+    q, s = quantize_fp8_ref(y, granularity, block=block)
+    return q, s, y
+
+
 def expand_scale(scale: np.ndarray, rows: int, k: int, block: int = 128) -> np.ndarray:
     """Broadcast a scale tensor to ``[rows, k]`` (``forge/kernels/ref/gemm_fp8.py:88-101``)."""
     s = np.asarray(scale, dtype=np.float32)

@@ -61,3 +61,36 @@ def test_workspace_query_follows_the_kernel_plan(m, n, k, expect_ws):
     assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(cfg)) == 0
     # the generic kernel never needs one; a g_idx call routes there
     assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 1, None) == 0
+
+
+def _header_prototypes() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    protos = {}
+    for m in re.finditer(r"\b(fg_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        protos[m.group(1)] = params
+    return protos
+
+
+def _ctype_for(param: str):
+    t = param.rsplit(" ", 1)[0] if not param.endswith("*") else param
+    if "*" in param:
+        return ctypes.c_void_p if "fg_w4_config" not in param and "fg_mm_config" not in param else "struct*"
+    t = t.replace("const ", "").strip()
+    return {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "int": ctypes.c_int, "size_t": ctypes.c_size_t,
+            "float": ctypes.c_float, "fg_stream_t": ctypes.c_void_p}[t]
+
+
+def test_ctypes_signatures_match_the_header_parameter_types():
+    """A 64-bit parameter bound as a 32-bit ctypes int would leave garbage in the upper half of its register."""
+    protos = _header_prototypes()
+    assert set(protos) == set(_lib.SIGNATURES)
+    for name, params in protos.items():
+        args, _ = _lib.SIGNATURES[name]
+        assert len(args) == len(params), name
+        for a, p in zip(args, params):
+            want = _ctype_for(p)
+            if want == "struct*":
+                assert getattr(a, "_type_", None) in (_lib.W4Config, _lib.MMConfig), (name, p)
+            else:
+                assert ctypes.sizeof(a) == ctypes.sizeof(want) and a in (want, ctypes.c_int32, ctypes.c_int), (name, p, a)
