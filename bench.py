@@ -11,10 +11,14 @@ value = algorithmic bytes per step / step time, bytes per linear = N*K/2 + 2*G*N
 Secondary (``w8a8``): FP8 e4m3fn GEMM at M=4096, K=N=8192 and INT8 GEMM at M=4096 on the Llama-3-70B
 shapes, in TFLOP/s against the dense fp8 / int8 MFMA peaks, on pre-quantised operands.
 
-``roofline``: the dominant kernel (the gate+up GEMV, 61 MB per launch) timed with HIP events on its launch stream.
+``roofline``: the dominant kernel (the gate+up GEMV, 61 MB per launch) timed with HIP events on its launch stream;
+``traffic`` (HBM bytes per launch) comes from the FETCH_SIZE / WRITE_SIZE counter passes summarised in
+profiles/w4_gemv_gate_up_pmc.json (made with ``--pmc-workload``), when that file is present.
 ``cpu_baseline``: the C oracle (oracle/c/oracle.c, scalar, one thread) on a bounded sample of the same workload.
 
 Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1]``; prints one JSON line.
+``python bench.py --pmc-workload``: only a 256 MiB device copy (counter calibration) and 64 gate+up GEMV launches,
+eager, for ``rocprofv3 --pmc`` passes.
 """
 from __future__ import annotations
 
@@ -124,6 +128,35 @@ def bench_w8a8(torch, ops, dev, reps: int) -> dict:
     return out
 
 
+def pmc_workload(torch, layouts, ops, dev, gen) -> None:
+    """Counter-pass workload: a 256 MiB device-to-device copy (known bytes: calibrates FETCH_SIZE / WRITE_SIZE) three
+    times, then the gate+up GEMV (K=4096, N=28672, M=1) over a ring of 32 weights, twice (64 launches)."""
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    k, n = SHAPES["gate_up"]
+    x = torch.randn(1, k, device=dev, generator=gen).bfloat16()
+    ring = [make_layer_weights(torch, layouts, dev, k, n, gen) for _ in range(LAYERS)]
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for p in ring:
+            ops.w4a16_linear(x, p)
+    torch.cuda.synchronize()
+    log("pmc workload done: 3 x 256 MiB copy, 64 gate_up GEMV launches")
+
+
+def load_traffic() -> dict | None:
+    """HBM bytes per gate+up launch from the committed counter summary (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "w4_gemv_gate_up_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict:
     """The scalar C oracle (one thread) on one decode layer's four W4A16 linears at M=1, repeated to ~`seconds`."""
     import numpy as np
@@ -164,6 +197,7 @@ def main() -> None:
     ap.add_argument("--no-w8a8", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
+    ap.add_argument("--pmc-workload", action="store_true", help="run only the counter-pass workload (no timing)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the hot path is a single-GPU kernel; multi-GPU sharding is "
@@ -179,6 +213,9 @@ def main() -> None:
     torch.cuda.set_device(dev)
     log(f"device: {torch.cuda.get_device_name(dev)}")
     gen = torch.Generator(device=dev).manual_seed(1234)
+    if args.pmc_workload:
+        pmc_workload(torch, layouts, ops, dev, gen)
+        return
     ring = []  # (name, x, packed)
     xs = {k: torch.randn(1, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
     for layer in range(LAYERS):
@@ -211,10 +248,12 @@ def main() -> None:
                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"  {name:8s} K={k:5d} N={n:5d}: {t * 1e3:8.3f} us  {gbs:7.1f} GB/s")
     dom = per_shape["gate_up"]
+    tr = load_traffic()
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "w4_gemv_kernel<1,4,bf16> (gate_up K=4096 N=28672, M=1)",
-                "bytes_per_launch": w4_bytes(1, 4096, 28672), "avg_launch_us": dom["us"]}
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None if tr is None else tr["traffic_bytes"],
+                "kernel": "w4_gemv_tile_kernel<1,2,bf16> (gate_up K=4096 N=28672, M=1)",
+                "bytes_per_launch": w4_bytes(1, 4096, 28672), "avg_launch_us": dom["us"],
+                "traffic_source": None if tr is None else "profiles/w4_gemv_gate_up_pmc.json"}
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
