@@ -39,6 +39,14 @@ hipError_t launch_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64
 hipError_t launch_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
                            int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
                            int64_t ldy, int ydt, int M, int N, int K, int tile, hipStream_t s);
+bool mm_big_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t K);
+int64_t mm_big_tiles(int64_t M, int64_t N);
+hipError_t launch_int8_gemm_big(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                                int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                                int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
+hipError_t launch_fp8_gemm_big(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
+                               int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
+                               int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
 hipError_t launch_fp8_gemm_blocked(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, int64_t sa_sk,
                                    const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_sn, int64_t sb_sk,
                                    int sb_div, const void* bias, int bdt, void* y, int64_t ldy, int ydt, int M, int N,
@@ -75,6 +83,17 @@ int hip_status(hipError_t e, const char* what) {
 bool is_float_dt(int dt) { return dt == FG_F32 || dt == FG_F16 || dt == FG_BF16; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+// W8A8 tile policy: tile_m = 256 (config or automatic) selects the 256 x 256 direct-to-LDS kernel, which needs
+// K % 128 == 0 and 16-byte aligned operands with 16-byte multiple leading dimensions; it is chosen automatically once
+// its tiles cover every CU of an MI355X (256) at least once.  Otherwise 64 x 64 (M or N <= 64) or 128 x 128 tiles.
+int mm_tile(int64_t M, int64_t N, int64_t K, const void* a, int64_t lda, const void* b, int64_t ldb,
+            const fg_mm_config* cfg) {
+  const bool big_ok = fg::mm_big_ok(a, lda, b, ldb, K);
+  if (cfg && cfg->tile_m) return (cfg->tile_m == 256 && !big_ok) ? -1 : cfg->tile_m;
+  if (big_ok && fg::mm_big_tiles(M, N) >= 256) return 256;
+  return (M <= 64 || N <= 64) ? 64 : 128;
+}
 
 }  // namespace
 
@@ -241,7 +260,13 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
     if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad bias dtype");
   }
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
-  const int tile = cfg && cfg->tile_m ? cfg->tile_m : (M <= 64 || N <= 64 ? 64 : 128);
+  const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
+  if (tile < 0)
+    return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0 and 16-byte aligned operands");
+  if (tile == 256)
+    return hip_status(fg::launch_int8_gemm_big(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy,
+                                               y_dtype, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream)),
+                      "fg_int8_gemm launch");
   return hip_status(fg::launch_int8_gemm(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy, y_dtype,
                                          (int)M, (int)N, (int)K, tile, static_cast<hipStream_t>(stream)),
                     "fg_int8_gemm launch");
@@ -261,7 +286,13 @@ int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (scale_mode == 0 || scale_mode == 1) {
     if (scale_mode == 0) sa_sm = sb_sn = 0;
-    const int tile = cfg && cfg->tile_m ? cfg->tile_m : (M <= 64 || N <= 64 ? 64 : 128);
+    const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
+    if (tile < 0)
+      return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0 and 16-byte aligned operands");
+    if (tile == 256)
+      return hip_status(fg::launch_fp8_gemm_big(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy, y_dtype,
+                                                (int)M, (int)N, (int)K, s),
+                        "fg_fp8_gemm launch");
     return hip_status(fg::launch_fp8_gemm(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy, y_dtype,
                                           (int)M, (int)N, (int)K, tile, s),
                       "fg_fp8_gemm launch");

@@ -1,0 +1,254 @@
+// Large-output W8A8 GEMMs (INT8 and FP8 e4m3fn), C[M,N] = A[M,K] @ B[N,K]^T with both operands K-contiguous.
+//
+// Workgroup tile 256 x 256, 512 threads = 2 x 4 wavefronts of 128 x 64 (8 x 4 MFMA tiles of 16 x 16, 128 accumulator
+// registers per lane).  K is walked in 128-byte slices.  Each slice of A and B (2 x 32 KiB) is written straight from
+// global memory into one half of a double-buffered 128 KiB LDS ring by global_load_lds_dwordx4 (no staging registers,
+// no VALU), one wavefront instruction = 1 KiB = 8 rows x 128 bytes.  Within a 128-byte LDS row the 16-byte unit c of
+// global row r is stored at position c ^ (r & 7): the load lanes pick their global column so that this holds, and the
+// fragment reads (16 rows of one 16-row slab per instruction) then fall on 8 distinct bank groups.
+//
+// Epilogue for 16-bit outputs: the fp32 result of each 16-row slab of a wavefront tile is scaled, rounded and written
+// to a per-wavefront LDS buffer, then stored as 16-byte row segments (row scales read once per row, column scales and
+// bias once per column).  32-bit outputs are stored element by element.
+//
+// Requirements (checked by mm_big_ok): K % 128 == 0, 16-byte aligned A and B with lda, ldb multiples of 16.  Rows of A
+// or B past M or N are read from row M-1 or N-1 (valid memory) and their results are not stored.
+#include "fg_mm.h"
+
+namespace fg {
+
+template <class E, class = void>
+struct IsVec16 : std::false_type {};
+template <class E>
+struct IsVec16<E, std::void_t<decltype(E::kVec16)>> : std::integral_constant<bool, E::kVec16> {};
+
+// Fragment of row `rp` (one row of a 16-row slab, 128 bytes in LDS, units swizzled by r16 = row % 16) for k-step s.
+struct MmaI8Big : MmaI8 {  // 16 bytes per lane: unit 4s + lane/16
+  static __device__ __forceinline__ frag_t load_sw(const uint8_t* rp, int r16, int lane, int s) {
+    const int c = (4 * s + (lane >> 4)) ^ (r16 & 7);
+    return *reinterpret_cast<const i32x4*>(rp + c * 16);
+  }
+};
+struct MmaF8Big : MmaF8 {  // 32 bytes per lane: units 2 * (lane/16) and +1 (one k-step per 128-byte slice)
+  static __device__ __forceinline__ frag_t load_sw(const uint8_t* rp, int r16, int lane, int) {
+    const int c0 = (2 * (lane >> 4)) ^ (r16 & 7), c1 = (2 * (lane >> 4) + 1) ^ (r16 & 7);
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(rp + c0 * 16);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(rp + c1 * 16);
+    frag_t f;
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+    f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+    return f;
+  }
+};
+
+// 16-bit-output epilogues: value = (acc * row_scale) * col_scale (+ bias), one rounding per operation, in the order of
+// EpiInt8 / EpiFp8 (and of the oracles), then one rounding to bf16 / fp16.
+struct EpiInt8V {
+  static constexpr bool kVec16 = true;
+  const float* sa; int64_t sa_len;
+  const float* sb; int64_t sb_len;
+  const void* bias; int bdt;
+  uint16_t* y; int64_t ldy; bool bf16; bool vec_ok;
+  __device__ __forceinline__ float row_scale(int m) const { return sa[sa_len == 1 ? 0 : m]; }
+  __device__ __forceinline__ float col_scale(int n) const { return sb[sb_len == 1 ? 0 : n]; }
+  __device__ __forceinline__ float col_bias(int n) const { return bias ? load_f(bias, bdt, n) : 0.f; }
+  __device__ __forceinline__ float value(int acc, float rs, float cs, float cb) const {
+    float v = (float)acc * rs;
+    v = v * cs;
+    return bias ? v + cb : v;
+  }
+  __device__ __forceinline__ uint16_t cvt(float v) const { return bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v); }
+  __device__ __forceinline__ uint16_t* row_ptr(int m) const { return y + (int64_t)m * ldy; }
+};
+
+struct EpiFp8V {
+  static constexpr bool kVec16 = true;
+  const float* sa; int64_t sa_sm;
+  const float* sb; int64_t sb_sn;
+  const void* bias; int bdt;
+  uint16_t* y; int64_t ldy; bool bf16; bool vec_ok;
+  __device__ __forceinline__ float row_scale(int m) const { return sa[(int64_t)m * sa_sm]; }
+  __device__ __forceinline__ float col_scale(int n) const { return sb[(int64_t)n * sb_sn]; }
+  __device__ __forceinline__ float col_bias(int n) const { return bias ? load_f(bias, bdt, n) : 0.f; }
+  __device__ __forceinline__ float value(float acc, float rs, float cs, float cb) const {
+    float v = acc * rs;
+    v = v * cs;
+    return bias ? v + cb : v;
+  }
+  __device__ __forceinline__ uint16_t cvt(float v) const { return bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v); }
+  __device__ __forceinline__ uint16_t* row_ptr(int m) const { return y + (int64_t)m * ldy; }
+};
+
+constexpr int kBigBM = 256, kBigBN = 256, kBigWM = 2, kBigWN = 4, kBigBK = 128;
+constexpr size_t kBigLds = 2 * (size_t)(kBigBM + kBigBN) * kBigBK;
+
+template <class Mma, class Epi>
+__global__ void __launch_bounds__(kBigWM * kBigWN * 64) mm_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
+                                                                      const uint8_t* __restrict__ B, int64_t ldb,
+                                                                      int M, int N, int K, Epi epi) {
+  constexpr int BM = kBigBM, BN = kBigBN, WM = kBigWM, WN = kBigWN, BK = kBigBK;
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int A_INSTR = BM * BK / 16 / NT, B_INSTR = BN * BK / 16 / NT;  // 1 KiB load instructions per wave
+  static_assert(A_INSTR * NT * 16 == BM * BK && B_INSTR * NT * 16 == BN * BK, "tile / thread count mismatch");
+  constexpr int STAGE = (BM + BN) * BK;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
+  int tm_, tn_;
+  tile_of(blockIdx.x, ntm, ntn, tm_, tn_);
+  const int m0 = tm_ * BM, n0 = tn_ * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Load instruction i of wave w fills LDS units (w * INSTR + i) * 64 + lane, i.e. row (w * INSTR + i) * 8 + lane / 8,
+  // position lane % 8, which holds global unit (lane % 8) ^ (row % 8) = (lane % 8) ^ (lane / 8).
+  const int lrow = lane >> 3, lcol = ((lane & 7) ^ (lane >> 3)) * 16;
+  const int arow0 = wave * A_INSTR * 8 + lrow, brow0 = wave * B_INSTR * 8 + lrow;
+  auto issue = [&](int kt, uint8_t* st) __attribute__((always_inline)) {
+    const int64_t ko = (int64_t)kt * BK + lcol;
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i)
+      __builtin_amdgcn_global_load_lds(A + (int64_t)min(m0 + arow0 + 8 * i, M - 1) * lda + ko,
+                                       st + (wave * A_INSTR + i) * 1024, 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      __builtin_amdgcn_global_load_lds(B + (int64_t)min(n0 + brow0 + 8 * i, N - 1) * ldb + ko,
+                                       st + BM * BK + (wave * B_INSTR + i) * 1024, 16, 0, 0);
+  };
+
+  typename Mma::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0;
+
+  const int r16 = lane & 15;
+  const int nk = K / BK;
+  issue(0, smem);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* cur = smem + (kt & 1) * STAGE;
+    if (kt + 1 < nk) issue(kt + 1, smem + ((kt + 1) & 1) * STAGE);  // the other buffer: free since the last barrier
+    const uint8_t* sA = cur + (wm * TM * 16) * BK;
+    const uint8_t* sB = cur + BM * BK + (wn * TN * 16) * BK;
+#pragma unroll
+    for (int s = 0; s < BK / Mma::KB; ++s) {
+      typename Mma::frag_t fa[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = Mma::load_sw(sA + (i * 16 + r16) * BK, r16, lane, s);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const typename Mma::frag_t fb = Mma::load_sw(sB + (j * 16 + r16) * BK, r16, lane, s);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = Mma::mma(fa[i], fb, acc[i][j]);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next slice landed in LDS
+    __syncthreads();                                  // ... for every wave; and this slice is no longer read
+  }
+
+  if constexpr (IsVec16<Epi>::value) {
+    constexpr int SW = 16 * TN;  // slab width in columns
+    constexpr int SP = SW + 8;   // LDS row pitch in halves (16-byte aligned rows, staggered banks)
+    uint16_t* slab = reinterpret_cast<uint16_t*>(smem) + wave * 16 * SP;  // the ring is free after the last barrier
+    const int mw = m0 + wm * 16 * TM, nw = n0 + wn * SW;
+    float cs[TN], cb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = min(nw + j * 16 + (lane & 15), N - 1);
+      cs[j] = epi.col_scale(n);
+      cb[j] = epi.col_bias(n);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float rs[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rs[e] = epi.row_scale(min(mw + i * 16 + 4 * (lane >> 4) + e, M - 1));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          slab[(4 * (lane >> 4) + e) * SP + j * 16 + (lane & 15)] = epi.cvt(epi.value(acc[i][j][e], rs[e], cs[j], cb[j]));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's slab writes are done before it reads them
+#pragma unroll
+      for (int u0 = 0; u0 < 16 * SW / 8; u0 += 64) {
+        const int u = u0 + lane, r = u / (SW / 8), c8 = u % (SW / 8);
+        const int m = mw + i * 16 + r, n = nw + c8 * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(slab + r * SP + c8 * 8);
+        if (m < M) {
+          if (n + 8 <= N && epi.vec_ok) {
+            *reinterpret_cast<uint4*>(epi.row_ptr(m) + n) = v;
+          } else {
+            const uint16_t h[8] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16),
+                                   (uint16_t)v.z, (uint16_t)(v.z >> 16), (uint16_t)v.w, (uint16_t)(v.w >> 16)};
+            for (int t = 0; t < 8 && n + t < N; ++t) epi.row_ptr(m)[n + t] = h[t];
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next slab overwrites the buffer
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + wm * 16 * TM + i * 16 + 4 * (lane >> 4) + e;
+          const int n = n0 + wn * 16 * TN + j * 16 + (lane & 15);
+          if (m < M && n < N) epi.store(m, n, acc[i][j][e]);
+        }
+  }
+}
+
+bool mm_big_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t K) {
+  return K % kBigBK == 0 && lda % 16 == 0 && ldb % 16 == 0 &&
+         ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) % 16) == 0;
+}
+
+// Workgroups of the 256 x 256 kernel for an M x N output.
+int64_t mm_big_tiles(int64_t M, int64_t N) { return ((M + kBigBM - 1) / kBigBM) * ((N + kBigBN - 1) / kBigBN); }
+
+template <class Mma, class Epi>
+static hipError_t launch_big(const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, int M, int N, int K,
+                             const Epi& epi, hipStream_t s) {
+  auto k = mm_big_kernel<Mma, Epi>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)kBigLds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)mm_big_tiles(M, N)), dim3(kBigWM * kBigWN * 64), kBigLds, s, A, lda, B, ldb, M,
+                     N, K, epi);
+  return hipGetLastError();
+}
+
+static bool vec16_ok(const void* y, int64_t ldy) { return ldy % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0; }
+
+hipError_t launch_int8_gemm_big(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                                int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                                int64_t ldy, int ydt, int M, int N, int K, hipStream_t s) {
+  const uint8_t* A = reinterpret_cast<const uint8_t*>(a);
+  const uint8_t* B = reinterpret_cast<const uint8_t*>(b);
+  if (ydt == FG_BF16 || ydt == FG_F16) {
+    EpiInt8V epi{sa, sa_len, sb, sb_len, bias, bdt, static_cast<uint16_t*>(y), ldy, ydt == FG_BF16, vec16_ok(y, ldy)};
+    return launch_big<MmaI8Big>(A, lda, B, ldb, M, N, K, epi, s);
+  }
+  EpiInt8 epi{sa, sa_len, sb, sb_len, bias, bdt, y, ldy, ydt};
+  return launch_big<MmaI8Big>(A, lda, B, ldb, M, N, K, epi, s);
+}
+
+hipError_t launch_fp8_gemm_big(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
+                               int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
+                               int64_t ldy, int ydt, int M, int N, int K, hipStream_t s) {
+  if (ydt == FG_BF16 || ydt == FG_F16) {
+    EpiFp8V epi{sa, sa_sm, sb, sb_sn, bias, bdt, static_cast<uint16_t*>(y), ldy, ydt == FG_BF16, vec16_ok(y, ldy)};
+    return launch_big<MmaF8Big>(a, lda, b, ldb, M, N, K, epi, s);
+  }
+  EpiFp8 epi{sa, sa_sm, sb, sb_sn, bias, bdt, y, ldy, ydt};
+  return launch_big<MmaF8Big>(a, lda, b, ldb, M, N, K, epi, s);
+}
+
+}  // namespace fg

@@ -48,7 +48,8 @@ typedef struct fg_w4_config {
 } fg_w4_config;
 
 typedef struct fg_mm_config {
-  int32_t tile_m; /* 0 = policy */
+  int32_t tile_m; /* 0 = policy; 64 / 128 = square tiles of that size; 256 = the 256 x 256 direct-to-LDS kernel
+                     (needs K % 128 == 0 and 16-byte aligned A, B with lda, ldb multiples of 16, else FG_EUNSUPPORTED) */
   int32_t tile_n;
   int32_t reserved[6];
 } fg_mm_config;
