@@ -39,6 +39,9 @@ INT8_PEAK_TOPS = 5000.0  # dense
 SHAPES = {"qkv": (4096, 6144), "o_proj": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
 LAYERS = 32
 GROUP = 128
+# the launch the C library's policy makes for gate+up at M=1: one row of x, one 16-byte chunk per lane, 16 output
+# channels per wavefront (two K slices of 2048 columns, four channel blocks per workgroup)
+DOM_KERNEL = "w4_gemv_split_kernel<1,1,16,bf16>"
 METRIC = "W4A16 GEMV HBM GB/s (% peak) at M=1; W8A8 TFLOPS (% MFMA peak) at M=4096"
 
 
@@ -149,12 +152,14 @@ def pmc_workload(torch, layouts, ops, dev, gen) -> None:
 
 
 def load_traffic() -> dict | None:
-    """HBM bytes per gate+up launch from the committed counter summary (None when absent)."""
+    """HBM bytes per gate+up launch from the committed counter summary (None when absent or measured on another
+    kernel than the one the policy runs now)."""
     path = os.path.join(ROOT, "profiles", "w4_gemv_gate_up_pmc.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f)
+        tr = json.load(f)
+    return tr if tr.get("kernel", "").split(" ")[0] == DOM_KERNEL.split("<")[0] else None
 
 
 def cpu_baseline(seconds: float = 12.0) -> dict:
@@ -251,7 +256,7 @@ def main() -> None:
     tr = load_traffic()
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None if tr is None else tr["traffic_bytes"],
-                "kernel": "w4_gemv_tile_kernel<1,2,bf16> (gate_up K=4096 N=28672, M=1)",
+                "kernel": f"{DOM_KERNEL} (gate_up K=4096 N=28672, M=1)",
                 "bytes_per_launch": w4_bytes(1, 4096, 28672), "avg_launch_us": dom["us"],
                 "traffic_source": None if tr is None else "profiles/w4_gemv_gate_up_pmc.json"}
 

@@ -32,6 +32,13 @@ hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, c
                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
                                int K, int gs, int G, int tile_n, hipStream_t s);
 bool w4_gemv_tile_ok(int mt, int N, int K, int G, int tile_n);
+hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                                int K, int gs, bool single_group, hipStream_t s);
+bool w4_gemv_split_ok(int mt, int N, int K);
+bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
+                        int64_t lds, int N, int K);
 size_t w4_gemv_tile_lds_bytes(int mt, int K, int G, int TN);
 hipError_t launch_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
@@ -125,8 +132,8 @@ namespace {
 // workspace a caller sizes is the workspace the launch uses.
 struct W4Plan {
   int impl;
-  int mt, rows, max_blocks;  // GEMV
-  int tile_m, splits;        // MFMA
+  int gemv, mt, rows, max_blocks;  // GEMV: FG_GEMV_* kernel, rows of x per pass, wave-kernel knobs
+  int tile_m, splits;              // MFMA
   size_t ws_bytes;
 };
 
@@ -136,22 +143,32 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
   const int G = (int)((K + gs - 1) / gs);
   const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  const bool gemv_shape = !has_g_idx && q_aligned && (gs % 32 == 0 || G == 1) && M <= 4;
+  const bool split_fits = fg::w4_gemv_split_ok(mt, (int)N, (int)K);
   const bool tile_fits = fg::w4_gemv_tile_ok(mt, (int)N, (int)K, G, cfg ? cfg->tile_n : 0);
-  const bool gemv_ok = !has_g_idx && q_aligned && (gs % 32 == 0 || group_size <= 0) && M <= 4 &&
-                       (tile_fits || fg::w4_gemv_lds_bytes(4, (int)K) <= 150 * 1024);
+  const bool wave_fits = fg::w4_gemv_lds_bytes(4, (int)K) <= 150 * 1024;
+  int gemv = cfg ? cfg->gemv_kernel : FG_GEMV_AUTO;
+  if (gemv == FG_GEMV_AUTO && cfg && cfg->rows_per_wave) gemv = FG_GEMV_WAVE;
+  if (gemv == FG_GEMV_AUTO && cfg && cfg->tile_n) gemv = FG_GEMV_TILE;
+  if (gemv < FG_GEMV_AUTO || gemv > FG_GEMV_WAVE) return fail(FG_EINVAL, "fg_w4a16_gemm: unknown gemv_kernel %d", gemv);
+  // AUTO is resolved at launch, where the operand addresses decide between the split and the tiled kernel
+  const bool gemv_ok = gemv_shape && (gemv == FG_GEMV_SPLIT   ? split_fits
+                                      : gemv == FG_GEMV_TILE  ? tile_fits
+                                      : gemv == FG_GEMV_WAVE  ? wave_fits
+                                                              : (split_fits || tile_fits || wave_fits));
   const bool mfma_ok = !has_g_idx && q_aligned && x_aligned && (K % 8 == 0);
   int use = impl;
   if (use == FG_W4_AUTO) use = gemv_ok ? FG_W4_GEMV : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC);
   if (use == FG_W4_GEMV && !gemv_ok)
-    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: GEMV needs M<=4, no g_idx, group%%32==0, ldq%%4==0, aligned qweight");
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: GEMV kernel %d needs M<=4, no g_idx, group%%32==0, ldq%%4==0, "
+                                 "aligned qweight and a K / N it covers", gemv);
   if (use == FG_W4_MFMA && !mfma_ok)
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: MFMA path needs no g_idx, K%%8==0, ldq%%4==0, ldx%%8==0 and "
                                  "16-byte aligned x/qweight");
   if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC)
     return fail(FG_EINVAL, "fg_w4a16_gemm: unknown impl %d", impl);
-  *p = W4Plan{use, 1, 4, 0, 0, 1, 0};
+  *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0};
   if (use == FG_W4_GEMV) {
-    p->mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
     p->rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 4;
     if (p->rows != 1 && p->rows != 2 && p->rows != 4) return fail(FG_EINVAL, "fg_w4a16_gemm: rows_per_wave must be 1, 2 or 4");
     p->max_blocks = cfg ? cfg->max_blocks : 0;
@@ -211,8 +228,19 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
-  const bool tile_fits = fg::w4_gemv_tile_ok(p.mt, (int)N, (int)K, (int)G, cfg ? cfg->tile_n : 0);
-  if (p.impl == FG_W4_GEMV && tile_fits && !(cfg && cfg->rows_per_wave)) {
+  if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_AUTO) {
+    // the split kernel in its branch-free form, else the tiled kernel, else whichever covers the shape
+    if (fg::w4_gemv_split_preferred(p.mt, x, ldx, perm, scales, scale_dtype, lds, (int)N, (int)K))
+      p.gemv = FG_GEMV_SPLIT;
+    else if (fg::w4_gemv_tile_ok(p.mt, (int)N, (int)K, (int)G, 0))
+      p.gemv = FG_GEMV_TILE;
+    else
+      p.gemv = fg::w4_gemv_split_ok(p.mt, (int)N, (int)K) ? FG_GEMV_SPLIT : FG_GEMV_WAVE;
+  }
+  if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_SPLIT) {
+    e = fg::launch_w4_gemv_split(p.mt, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
+                                 bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
+  } else if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_TILE) {
     e = fg::launch_w4_gemv_tile(p.mt, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
                                 bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, (int)G, cfg ? cfg->tile_n : 0, s);
   } else if (p.impl == FG_W4_GEMV) {

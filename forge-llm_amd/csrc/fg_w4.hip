@@ -483,6 +483,321 @@ __global__ void __launch_bounds__(w4_tile_max_waves(MT, S) * kWave) w4_gemv_tile
   }
 }
 
+static int device_cus();
+
+// ------------------------------------------------------------------------------------------------ GEMV (split-K)
+enum { kSplitGeneral = 0, kSplitF16Scales = 1, kSplitBf16Scales = 2 };  // w4_gemv_split_kernel MODE
+// Decode GEMV for M <= MT <= 4 with no LDS on the hot path.  A wavefront owns R consecutive output channels and one K
+// slice of at most S 32-column chunks per lane (chunk c = slice start + lane + 64 i); the K slices of a channel block
+// are the KS wavefronts of one workgroup, summed in a fixed order through LDS at the end.  The lane's x chunks are read
+// once (they are cache resident: every wavefront reads the same x), put into the nibble-pair order of the weight
+// unpack, and kept in registers with their sums; the R scales of a chunk's group and the zero-point word come straight
+// from global memory next to the weights.  Every wavefront is independent until the final sum, so many of them per CU
+// keep HBM busy while others compute.
+// The FAST modes (N % R == 0, K % 32 == 0, fp16 or bf16 scales with lds % 8 == 0, 16-byte aligned x and scales,
+// ldx % 8 == 0, no perm; the scale type is a template parameter) issue every load of the wavefront unconditionally,
+// back to back, in the order of first use: a load under a branch, or a branch on the scale type between loads and
+// their use, makes the compiler wait for all earlier loads.  Symmetric weights then read a dummy word (`zeros` points
+// at any valid memory, ldz = 0) and replace it by 0x88888888.  The general form takes ragged N, K tails, fp32 scales,
+// unaligned or permuted x with per-element loads.
+//   gs32: group size / 32 (groups are whole chunks), 0 for one group per row.
+// Threads per workgroup at most (BW * KS wavefronts): 512 for four rows of x, which need more than 128 registers.
+constexpr int w4_split_max_threads(int mt) { return mt == 4 ? 512 : 1024; }
+
+template <int MT, int S, int R, bool XBF16, int MODE>
+__global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ perm, const int32_t* __restrict__ qw,
+    int64_t ldq, const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz,
+    int hasz, const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
+    int gs32, int KS) {
+  static_assert(R * MT == 4 || R * MT == 8 || R * MT == 16, "rows x batch must be 4, 8 or 16");
+  constexpr bool FAST = MODE != kSplitGeneral;
+  constexpr uint32_t kMagicBytes = XBF16 ? 0x43434343u : 0x64646464u;
+  constexpr uint32_t kOnes = XBF16 ? 0x3f803f80u : 0x3c003c00u;  // (1, 1) as bf16 / fp16 pairs
+  constexpr float kB = XBF16 ? 128.f : 1024.f;
+  __shared__ float red[16][R * MT];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
+  const int BW = (int)(blockDim.x / kWave) / KS;
+  const int ks = wave % KS, blk = blockIdx.x * BW + wave / KS;
+  const int n0 = blk * R;
+  const int nr = min(n0, N - R);  // FAST: first row read (blocks past the end re-read the last block)
+  const int c0 = (int)((int64_t)ks * KC / KS), c1 = (int)((int64_t)(ks + 1) * KC / KS);
+  const int64_t ldq4 = ldq / 4;
+  const uint4* __restrict__ qw4 = reinterpret_cast<const uint4*>(qw);
+  const FastDiv gdiv((uint32_t)max(gs32, 1));
+
+  int cl[S], gl[S];
+  bool ok[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int c = c0 + lane + kWave * i;
+    ok[i] = c < c1;
+    cl[i] = min(c, KC - 1);
+    gl[i] = gs32 > 0 ? (int)gdiv.div((uint32_t)cl[i]) : 0;
+  }
+  // Loads in the order of first use for one row of x: x (its chunk sums start every row), scales and zero words, then
+  // the weights row by row (general form: rows past N re-read row N-1).  With 2-4 rows of x the weights go first:
+  // holding the raw x of every row through the weight loads would spill.
+  uint4 xv[MT][S][4];
+  auto load_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const uint16_t* xr = x + (int64_t)min(m, M - 1) * ldx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int wi = 4 * cl[i] + q;
+          if constexpr (FAST) {
+            xv[m][i][q] = reinterpret_cast<const uint4*>(xr)[wi];
+          } else {
+            uint32_t h[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int k = 8 * wi + e;
+              h[e] = k < K ? xr[perm ? perm[k] : k] : 0u;
+            }
+            xv[m][i][q] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+          }
+        }
+      }
+  };
+  uint32_t sraw[S][FAST ? (R + 1) / 2 : R];  // FAST: two 16-bit scales per word
+  uint32_t zw[S][(R + 7) / 8];
+  auto load_sz = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int64_t srow = (int64_t)gl[i] * lds;
+      if constexpr (FAST) {
+        const uint16_t* sp = static_cast<const uint16_t*>(scales) + srow + nr;
+        if constexpr (R == 4) {
+          const uint2 t = *reinterpret_cast<const uint2*>(sp);
+          sraw[i][0] = t.x;
+          sraw[i][1] = t.y;
+        } else {
+#pragma unroll
+          for (int h = 0; h < R / 8; ++h) {
+            const uint4 t = *reinterpret_cast<const uint4*>(sp + 8 * h);
+            sraw[i][4 * h] = t.x;
+            sraw[i][4 * h + 1] = t.y;
+            sraw[i][4 * h + 2] = t.z;
+            sraw[i][4 * h + 3] = t.w;
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < (R + 7) / 8; ++h) zw[i][h] = (uint32_t)zeros[(int64_t)gl[i] * ldz + nr / 8 + h];
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) sraw[i][r] = load_raw(scales, sdt, srow + min(n0 + r, N - 1));
+#pragma unroll
+        for (int h = 0; h < (R + 7) / 8; ++h)
+          zw[i][h] = (uint32_t)zeros[(int64_t)gl[i] * ldz + min(n0 / 8 + h, (N - 1) / 8)];
+      }
+    }
+  };
+  uint4 w[R][S];
+  auto load_w = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        w[r][i] = load16_stream(qw4 + (int64_t)(FAST ? nr + r : min(n0 + r, N - 1)) * ldq4 + cl[i]);
+  };
+  if constexpr (MT == 1) {
+    load_x();
+    load_sz();
+    load_w();
+  } else {
+    load_w();
+    load_sz();
+    load_x();
+  }
+
+  // x chunks in nibble-pair order, and their sums
+  uint4 xu[MT][S][4];
+  float xs[MT][S];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = xv[m][i][q];
+        // (x0,x1)(x2,x3)(x4,x5)(x6,x7) -> (x0,x2)(x1,x3)(x4,x6)(x5,x7), the order of the nibble pairs below
+        xu[m][i][q] = make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                                 __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+        sum = dot2_acc<XBF16>(xu[m][i][q].x, kOnes, sum);
+        sum = dot2_acc<XBF16>(xu[m][i][q].y, kOnes, sum);
+        sum = dot2_acc<XBF16>(xu[m][i][q].z, kOnes, sum);
+        sum = dot2_acc<XBF16>(xu[m][i][q].w, kOnes, sum);
+      }
+      xs[m][i] = sum;
+    }
+
+  const int zsh = R == 4 ? ((FAST ? nr : n0) & 7) : 0;  // nibble of the block's first row in its zero word
+  float acc[R * MT];
+#pragma unroll
+  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (!ok[i]) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float sc;
+      if constexpr (MODE == kSplitF16Scales) {
+        sc = f16_bits_to_f32((uint16_t)((r & 1) ? sraw[i][r >> 1] >> 16 : sraw[i][r >> 1]));
+      } else if constexpr (MODE == kSplitBf16Scales) {
+        sc = __uint_as_float((r & 1) ? sraw[i][r >> 1] & 0xffff0000u : sraw[i][r >> 1] << 16);
+      } else {
+        sc = raw_bits_to_f32(sraw[i][r], sdt);
+      }
+      const uint32_t zword = hasz ? zw[i][r / 8] : 0x88888888u;
+      const float zb = kB + (float)nibble(zword, (r + zsh) & 7);
+      float d[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) d[m] = -zb * xs[m][i];
+      const uint32_t wq[4] = {w[r][i].x, w[r][i].y, w[r][i].z, w[r][i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = wq[q] & 0x0F0F0F0Fu, hi = (wq[q] >> 4) & 0x0F0F0F0Fu;
+        const uint32_t p0 = __builtin_amdgcn_perm(kMagicBytes, lo, 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(kMagicBytes, hi, 0x04010400u);
+        const uint32_t p2 = __builtin_amdgcn_perm(kMagicBytes, lo, 0x04030402u);
+        const uint32_t p3 = __builtin_amdgcn_perm(kMagicBytes, hi, 0x04030402u);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          d[m] = dot2_acc<XBF16>(xu[m][i][q].x, p0, d[m]);
+          d[m] = dot2_acc<XBF16>(xu[m][i][q].y, p1, d[m]);
+          d[m] = dot2_acc<XBF16>(xu[m][i][q].z, p2, d[m]);
+          d[m] = dot2_acc<XBF16>(xu[m][i][q].w, p3, d[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r * MT + m] = __builtin_fmaf(sc, d[m], acc[r * MT + m]);
+    }
+  }
+  const float tot = wave_transpose_sum<R * MT>(acc, lane);
+  constexpr int span = kWave / (R * MT);
+  auto store = [&](int idx, float v) {
+    const int r = idx / MT, m = idx - (idx / MT) * MT;
+    if (m < M && n0 + r < N) {
+      if (bias) v += load_f(bias, bdt, n0 + r);
+      y[(int64_t)m * ldy + n0 + r] = XBF16 ? f32_to_bf16_bits_hw(v) : f32_to_f16_bits(v);
+    }
+  };
+  if (KS == 1) {
+    if ((lane % span) == 0) store(lane / span, tot);
+  } else {
+    if ((lane % span) == 0) red[wave][lane / span] = tot;
+    __syncthreads();
+    if (ks == 0 && lane < R * MT) {  // the K slices of this block, summed in slice order
+      float v = 0.f;
+      for (int k2 = 0; k2 < KS; ++k2) v += red[wave + k2][lane];
+      store(lane, v);
+    }
+  }
+}
+
+// Launch shape of the split-K GEMV: S chunks per lane (1 while K <= 32768, else 2 for one row of x), KS =
+// ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront from the rows per CU (more rows amortise the x
+// registers: 16 rows for wide outputs, 4 for narrow ones; R * MT <= 16), BW channel blocks per workgroup (8 .. 16
+// wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
+bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) {
+  const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
+  const int s = KC <= 16 * kWave ? 1 : (KC <= 32 * kWave && mt == 1 ? 2 : 0);
+  if (s == 0) return false;
+  const int ks = (KC + kWave * s - 1) / (kWave * s);
+  const int per_cu = N / device_cus();
+  int r = per_cu >= 64 ? 16 : ((per_cu >= 20 || ks >= 4) ? 8 : 4);
+  if (mt == 2) r = min(r, 8);
+  if (mt == 4) r = 4;
+  if (s == 2) r = 4;  // 8 rows x 2 chunks would spill
+  const int max_waves = w4_split_max_threads(mt) / kWave;
+  if (ks > max_waves) return false;
+  int bw = max(2, 8 / ks);
+  while (bw * ks > max_waves && bw > 1) --bw;
+  *S = s; *R = r; *KS = ks; *BW = bw;
+  return true;
+}
+
+template <int MT, int S, int R, bool XBF16>
+static hipError_t launch_split_t(bool fast, const void* x, int64_t ldx, const int32_t* perm, const int32_t* qw,
+                                 int64_t ldq, const void* scales, int sdt, int64_t lds, const int32_t* zeros,
+                                 int64_t ldz, const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K,
+                                 int gs32, int KS, int BW, hipStream_t s) {
+  const int nblk = (N + R - 1) / R;
+  const int hasz = zeros != nullptr;
+  // symmetric weights: the zero word is read from qweight (always valid memory) and ignored
+  const int32_t* zp = hasz ? zeros : qw;
+  const int64_t ldzp = hasz ? ldz : 0;
+  const dim3 grid((nblk + BW - 1) / BW), block(kWave * BW * KS);
+  auto kern = !fast ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitGeneral>
+                    : (sdt == FG_BF16 ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales>
+                                      : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales>);
+  hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const uint16_t*>(x), ldx, perm, qw, ldq, scales, sdt, lds, zp,
+                     ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gs32, KS);
+  return hipGetLastError();
+}
+
+template <bool XBF16>
+static hipError_t launch_split_x(int mt, int S, int R, bool fast, const void* x, int64_t ldx, const int32_t* perm,
+                                 const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+                                 const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y, int64_t ldy,
+                                 int M, int N, int K, int gs32, int KS, int BW, hipStream_t s) {
+#define FG_SPLIT(MT_, S_, R_)                                                                                       \
+  return launch_split_t<MT_, S_, R_, XBF16>(fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, \
+                                            ldy, M, N, K, gs32, KS, BW, s)
+  if (mt == 1) {
+    if (S == 2) FG_SPLIT(1, 2, 4);
+    if (R == 4) FG_SPLIT(1, 1, 4);
+    if (R == 8) FG_SPLIT(1, 1, 8);
+    FG_SPLIT(1, 1, 16);
+  }
+  if (mt == 2) { if (R == 4) FG_SPLIT(2, 1, 4); FG_SPLIT(2, 1, 8); }
+  FG_SPLIT(4, 1, 4);
+#undef FG_SPLIT
+}
+
+// True when the split GEMV can take its branch-free form for these operands.
+static bool split_fast(int R, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
+                       int64_t lds, int N, int K) {
+  return perm == nullptr && (K % 32) == 0 && (N % R) == 0 && (ldx % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && sdt != FG_F32 && (lds % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(scales) % 16) == 0;
+}
+
+hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                                int K, int gs, bool single_group, hipStream_t s) {
+  int S, R, KS, BW;
+  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return hipErrorInvalidValue;
+  const int gs32 = single_group ? 0 : gs / 32;
+  const bool fast = split_fast(R, x, ldx, perm, scales, sdt, lds, N, K);
+  if (xbf16)
+    return launch_split_x<true>(mt, S, R, fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy,
+                                M, N, K, gs32, KS, BW, s);
+  return launch_split_x<false>(mt, S, R, fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy,
+                               M, N, K, gs32, KS, BW, s);
+}
+
+bool w4_gemv_split_ok(int mt, int N, int K) {
+  int S, R, KS, BW;
+  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW);
+}
+
+// Whether the policy takes the split GEMV: its branch-free form applies to these operands, and the shape is not one
+// where the tiled kernel measured faster (3-4 rows of x over wide outputs: at K=4096, N=28672 the tiled kernel takes
+// 22 us against 28 us; at N=4096..6144 the split kernel is as fast or faster).
+bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
+                        int64_t lds, int N, int K) {
+  int S, R, KS, BW;
+  if (mt == 4 && N / device_cus() >= 64) return false;
+  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW) && split_fast(R, x, ldx, perm, scales, sdt, lds, N, K);
+}
+
 // Generic kernel: any group size (multiple of 8), per-column g_idx, any ldq / alignment, any M.
 // One wavefront per (output channel n, block of 4 rows of x); each weight element is dequantised exactly as the
 // oracle does ((q - z) * s in fp32) and accumulated in fp32.

@@ -23,6 +23,8 @@ OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 # W4A16 impl codes
 W4_AUTO, W4_GEMV, W4_MFMA, W4_GENERIC = 0, 1, 2, 3
 W4_IMPL = {None: W4_AUTO, "auto": W4_AUTO, "gemv": W4_GEMV, "mfma": W4_MFMA, "generic": W4_GENERIC}
+GEMV_AUTO, GEMV_SPLIT, GEMV_TILE, GEMV_WAVE = 0, 1, 2, 3
+GEMV_KERNEL = {None: GEMV_AUTO, "auto": GEMV_AUTO, "split": GEMV_SPLIT, "tile": GEMV_TILE, "wave": GEMV_WAVE}
 
 
 class HipExtensionMissing(ForgeError):
@@ -44,7 +46,7 @@ class KernelLaunchError(ForgeError):
 class W4Config(ctypes.Structure):
     _fields_ = [("impl", ctypes.c_int32), ("rows_per_wave", ctypes.c_int32), ("max_blocks", ctypes.c_int32),
                 ("tile_m", ctypes.c_int32), ("split_k", ctypes.c_int32), ("tile_n", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("gemv_kernel", ctypes.c_int32), ("reserved", ctypes.c_int32 * 1)]
 
 
 class MMConfig(ctypes.Structure):

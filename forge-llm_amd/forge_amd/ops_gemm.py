@@ -150,8 +150,11 @@ def _w4_config(config: dict[str, Any] | None) -> _lib.W4Config | None:
     c = config or {}
     if c.get("impl") not in _IMPL_ALIASES:
         raise ConfigError(f"unknown W4A16 impl {c.get('impl')!r}; choose gemv, mfma or generic")
+    if c.get("gemv_kernel") not in _lib.GEMV_KERNEL:
+        raise ConfigError(f"unknown GEMV kernel {c.get('gemv_kernel')!r}; choose split, tile or wave")
     return _lib.W4Config(_lib.W4_IMPL[impl], int(c.get("rows_per_wave") or 0), int(c.get("max_blocks") or 0),
-                         int(c.get("tile_m") or 0), int(c.get("split_k") or 0), int(c.get("tile_n") or 0))
+                         int(c.get("tile_m") or 0), int(c.get("split_k") or 0), int(c.get("tile_n") or 0),
+                         _lib.GEMV_KERNEL[c.get("gemv_kernel")])
 
 
 def _w4_launch(x2: torch.Tensor, p: PackedW4, perm: torch.Tensor | None, g_idx: torch.Tensor | None,
@@ -180,8 +183,9 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     """``y = x @ dequant(W)^T + bias`` for ``x [..., K]`` bf16/fp16 on a gfx950 GPU (returns ``x.dtype``).
 
     Kernel by the C library's policy (override with ``config={"impl": "gemv"|"mfma"|"generic", ...}`` or
-    ``FORGE_W4_IMPL``): wave-per-channels GEMV for M <= 4, dequantise-to-LDS + bf16/fp16 MFMA otherwise, and a
-    per-element generic kernel for irregular act-order or unaligned weights.  All paths reduce in a fixed order
+    ``FORGE_W4_IMPL``): for M <= 4 a GEMV (``gemv_kernel``: "split" = register-resident split-K kernel, "tile" =
+    LDS-tiled kernel, "wave" = one wavefront per row block; chosen per shape and operand alignment), dequantise-to-LDS
+    + bf16/fp16 MFMA otherwise, and a per-element generic kernel for irregular act-order or unaligned weights.  All paths reduce in a fixed order
     (``deterministic`` is accepted for API compatibility; results are always run-to-run reproducible).
     """
     _ready(x, "w4a16_linear")

@@ -36,6 +36,9 @@ enum { FG_OK = 0, FG_EINVAL = 1, FG_EUNSUPPORTED = 2, FG_EHIP = 3 };
 /* W4A16 implementation selector (fg_w4_config.impl) */
 enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3 };
 
+/* GEMV kernel selector (fg_w4_config.gemv_kernel) */
+enum { FG_GEMV_AUTO = 0, FG_GEMV_SPLIT = 1, FG_GEMV_TILE = 2, FG_GEMV_WAVE = 3 };
+
 /* Launch knobs; pass NULL for the built-in per-shape policy.  Zero fields mean "policy default". */
 typedef struct fg_w4_config {
   int32_t impl;         /* FG_W4_* */
@@ -43,8 +46,11 @@ typedef struct fg_w4_config {
   int32_t max_blocks;   /* GEMV: cap on workgroups (grid-stride beyond it) */
   int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128) */
   int32_t split_k;      /* MFMA: K splits (fp32 partials in the workspace, reduced in fixed order) */
-  int32_t tile_n;       /* GEMV: output channels per workgroup tile (rounded up to a multiple of 8; 0 = policy) */
-  int32_t reserved[2];
+  int32_t tile_n;       /* GEMV tile kernel: output channels per workgroup tile (rounded up to a multiple of 8) */
+  int32_t gemv_kernel;  /* GEMV: FG_GEMV_SPLIT = split-K register kernel (M <= 4, K <= 65536), FG_GEMV_TILE = LDS-tiled
+                           kernel, FG_GEMV_WAVE = one-wavefront-per-row-block kernel; AUTO = split when it fits,
+                           else tile, else wave.  Setting rows_per_wave implies WAVE, tile_n implies TILE. */
+  int32_t reserved[1];
 } fg_w4_config;
 
 typedef struct fg_mm_config {

@@ -5,12 +5,15 @@ inside the reference's compare() rule (rel 2e-3, abs 1e-3, rel_norm 2e-2, eps-aw
 """
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
 
 from forge_amd import layouts as L
 from forge_amd import ops_gemm as ops
+from forge_amd.errors import ForgeError
 from oracle import gemm as og
 from oracle import w4 as ow
 from tests._util import assert_close, gen, oracle_packed, to_f32, w4_parts, x_act
@@ -20,12 +23,24 @@ DEV = "cuda"
 ODT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
 
 
-def _case(m, n, k, gs, sym, xdt, *, bias=False, seed=0, impl=None, scale_dtype=torch.float16, xscale=1.0):
+def _pad_rows(t: torch.Tensor, mult: int) -> torch.Tensor:
+    """The same 2-D values as a view of a buffer whose row stride is rounded up to a multiple of ``mult``."""
+    n, w = t.shape
+    buf = torch.zeros(n, -(-w // mult) * mult, dtype=t.dtype, device=t.device)
+    buf[:, :w] = t
+    return buf[:, :w]
+
+
+def _case(m, n, k, gs, sym, xdt, *, bias=False, seed=0, impl=None, scale_dtype=torch.float16, xscale=1.0,
+          config=None, pad_q=False):
     q, s, z = w4_parts(n, k, gs, sym, seed, scale_dtype)
     p = L.pack_w4(q, s, z, gs).to(DEV)
+    if pad_q:  # qweight rows padded to whole 16-byte chunks, the layout the GEMV kernels read
+        p = dataclasses.replace(p, qweight=_pad_rows(p.qweight, 4))
     x = x_act(m, k, xdt, seed + 1, xscale)
     b = (torch.randn(n, generator=gen(seed + 2)) * 0.5).to(xdt) if bias else None
-    y = ops.w4a16_linear(x.to(DEV), p, None if b is None else b.to(DEV), config={"impl": impl} if impl else None)
+    cfg = config if config is not None else ({"impl": impl} if impl else None)
+    y = ops.w4a16_linear(x.to(DEV), p, None if b is None else b.to(DEV), config=cfg)
     assert ops.last_path("w4a16_linear") == "hip" and y.dtype == xdt and y.shape == (m, n)
     ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs), None if b is None else to_f32(b))
     return y, ref
@@ -39,6 +54,57 @@ def _case(m, n, k, gs, sym, xdt, *, bias=False, seed=0, impl=None, scale_dtype=t
 def test_gemv_decode_matches_oracle(m, n, k, gs, sym, xdt):
     y, ref = _case(m, n, k, gs, sym, xdt, bias=(m % 2 == 1), seed=m + n, impl="gemv")
     assert_close(y.cpu(), ref, ODT[xdt], what=f"gemv m={m} n={n} k={k} gs={gs}")
+
+
+GEMV_CASES = [  # m, n, k, group, symmetric, x dtype, scale dtype
+    (1, 4096, 4096, 128, False, torch.bfloat16, torch.float16),
+    (3, 777, 2048, 32, True, torch.float16, torch.bfloat16),       # ragged N, unaligned scale rows, 4 rows of x
+    (2, 1030, 1000, -1, False, torch.bfloat16, torch.float32),     # one group; K ends inside the last 16-byte chunk
+    (4, 5, 1001, -1, True, torch.float16, torch.float16),          # N below the rows per wavefront, K % 8 != 0
+    (2, 2048, 8192, 128, False, torch.bfloat16, torch.float16),
+    (1, 3000, 14336, 128, False, torch.float16, torch.bfloat16),   # 7 K slices
+]
+
+
+@pytest.mark.parametrize("kernel", ["split", "tile", "wave"])
+@pytest.mark.parametrize("case", GEMV_CASES, ids=lambda c: f"m{c[0]}n{c[1]}k{c[2]}g{c[3]}")
+def test_gemv_kernels_match_oracle(kernel, case):
+    m, n, k, gs, sym, xdt, sdt = case
+    cfg = {"impl": "gemv", "gemv_kernel": kernel}
+    y, ref = _case(m, n, k, gs, sym, xdt, bias=True, seed=n + k, scale_dtype=sdt, config=cfg, pad_q=True)
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"gemv {kernel} m={m} n={n} k={k} gs={gs}")
+
+
+@pytest.mark.parametrize("m,n,k,gs,sdt", [(1, 256, 40000, 128, torch.float16), (1, 64, 65536, 64, torch.float32),
+                                          (4, 96, 16384, 32, torch.bfloat16), (2, 64, 32768, 128, torch.float16)])
+def test_split_gemv_long_k(m, n, k, gs, sdt):
+    """Two 16-byte chunks per lane and 10-16 K slices (K > 32768), and the K limits of 2 and 4 rows of x."""
+    cfg = {"impl": "gemv", "gemv_kernel": "split"}
+    y, ref = _case(m, n, k, gs, m == 4, torch.bfloat16, bias=m == 1, seed=k, scale_dtype=sdt, config=cfg)
+    assert_close(y.cpu(), ref, "bfloat16", what=f"split m={m} n={n} k={k}")
+
+
+def test_split_gemv_limits_and_unaligned_x():
+    q, s, z = w4_parts(512, 40000, 128, False, seed=41)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    with pytest.raises(ForgeError):  # two rows of x over K > 32768 is beyond the split kernel
+        ops.w4a16_linear(x_act(2, 40000, seed=42).to(DEV), p, config={"impl": "gemv", "gemv_kernel": "split"})
+    with pytest.raises(ForgeError):  # and so are four rows over K > 16384
+        ops.w4a16_linear(x_act(4, 40000, seed=42).to(DEV), p, config={"impl": "gemv", "gemv_kernel": "split"})
+    # the policy then takes another kernel
+    x2 = x_act(2, 40000, seed=42)
+    assert_close(ops.w4a16_linear(x2.to(DEV), p).cpu(), og.w4a16_gemm_ref(to_f32(x2), oracle_packed(q, s, z, 128)),
+                 "bfloat16", what="m=2 K=40000 policy")
+    # rows of x that start 2 bytes past a 16-byte boundary, with an odd row stride: element-wise x reads
+    k = 2048
+    q, s, z = w4_parts(1000, k, 64, False, seed=43)
+    p = L.pack_w4(q, s, z, 64).to(DEV)
+    xb = x_act(3, k + 1, seed=44)
+    xv = xb.to(DEV)[:, 1:]
+    assert xv.stride(0) == k + 1 and xv.data_ptr() % 16 != 0
+    y = ops.w4a16_linear(xv, p, config={"impl": "gemv", "gemv_kernel": "split"})
+    assert_close(y.cpu(), og.w4a16_gemm_ref(to_f32(xb[:, 1:].contiguous()), oracle_packed(q, s, z, 64)), "bfloat16",
+                 what="unaligned x")
 
 
 @pytest.mark.parametrize("m", [5, 16, 33, 64, 256])
