@@ -8,6 +8,8 @@ the step is captured once as a HIP graph and replayed (launch overhead excluded,
 value = algorithmic bytes per step / step time, bytes per linear = N*K/2 + 2*G*N + G*N/2 + 2*M*K + 2*M*N
 (packed weights, fp16 scales, packed zeros, bf16 x and y; forge/kernels/bench.py:164-166).
 
+Secondary (``w4_decode_sweep``, ``w4_prefill``): the same four shapes at M in {4, 16, 64} (configs[1], GB/s) and
+M in {512, 2048, 8192} (configs[2], TFLOP/s against 2.5 PFLOP/s dense bf16).
 Secondary (``w8a8``): FP8 e4m3fn GEMM at M=4096, K=N=8192 and INT8 GEMM at M=4096 on the Llama-3-70B
 shapes, in TFLOP/s against the dense fp8 / int8 MFMA peaks, on pre-quantised operands.
 
@@ -35,6 +37,7 @@ for _p in (ROOT, os.path.join(ROOT, "forge-llm_amd")):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP8_PEAK_TFLOPS = 5000.0  # dense
+BF16_PEAK_TFLOPS = 2500.0  # dense
 INT8_PEAK_TOPS = 5000.0  # dense
 SHAPES = {"qkv": (4096, 6144), "o_proj": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
 LAYERS = 32
@@ -99,6 +102,41 @@ def time_eager(torch, fn, reps: int, warmup: int) -> float:
     en.record()
     torch.cuda.synchronize()
     return st.elapsed_time(en) / reps
+
+
+def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -> tuple[dict, dict]:
+    """configs[1] decode sweep at M in {4, 16, 64} (GB/s of algorithmic bytes, HIP-graph replays over the 32-layer
+    ring) and configs[2] prefill at M in {512, 2048, 8192} (TFLOP/s against bf16 dense MFMA, one weight per shape)."""
+    decode = {}
+    for m in (4, 16, 64):
+        row = {}
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
+        for name, (k, n) in SHAPES.items():
+            sel = [(xs[k], p) for nm, _, p in ring if nm == name]
+
+            def run(sel=sel):
+                for x, p in sel:
+                    ops.w4a16_linear(x, p)
+
+            t = timer(torch, run, steps, warmup) / len(sel)
+            gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
+            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        decode[f"M{m}"] = row
+        log(f"decode M={m}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
+    prefill = {}
+    for m in (512, 2048, 8192):
+        row = {}
+        for name, (k, n) in SHAPES.items():
+            p = next(p for nm, _, p in ring if nm == name)
+            x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+            fn = lambda x=x, p=p: ops.w4a16_linear(x, p)  # noqa: E731
+            ms = time_eager(torch, fn, max(5, steps // 2), 2)
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            row[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+            del x
+        prefill[f"M{m}"] = row
+        log(f"prefill M={m}: " + "  ".join(f"{nm} {v['ms']:.3f} ms {v['tflops']:.0f} TF" for nm, v in row.items()))
+    return decode, prefill
 
 
 def bench_w8a8(torch, ops, dev, reps: int) -> dict:
@@ -201,6 +239,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-w8a8", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the W4A16 M=4..64 decode and prefill sweeps")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     ap.add_argument("--pmc-workload", action="store_true", help="run only the counter-pass workload (no timing)")
     args = ap.parse_args()
@@ -269,6 +308,9 @@ def main() -> None:
                       "shapes_KN": {k: list(v) for k, v in SHAPES.items()}, "parallelism": "single GPU",
                       "timing": "eager" if args.eager else "hip graph replay"},
            "frac_of_peak": round(value / HBM_PEAK_GBS, 4), "per_shape": per_shape, "roofline": roofline}
+    if not args.no_sweep:
+        out["w4_decode_sweep"], out["w4_prefill"] = bench_w4_sweep(torch, ops, ring, dev, gen, timer, args.steps,
+                                                                   args.warmup)
     del ring
     torch.cuda.empty_cache()
     if not args.no_w8a8:
