@@ -26,6 +26,13 @@ hipError_t launch_w4_mfma(const void* x, int64_t ldx, bool xbf16, const int32_t*
                           const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M, int N, int K, int gs,
                           int tile_m, int splits, hipStream_t s);
 void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchunk, int* used);
+bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
+               int64_t G);
+size_t w4_big_workspace_bytes(int M, int N, int K, int split_k);
+hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                         int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                         int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
+                         hipStream_t s);
 size_t w4_gemv_lds_bytes(int mt, int K);
 hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
@@ -128,6 +135,9 @@ int fg_device_ok(int device) {
 
 namespace {
 
+// Rows of x from which the policy takes the prefill kernel over the skinny MFMA kernel.
+constexpr int64_t kPrefillMinM = 128;
+
 // Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
 // workspace a caller sizes is the workspace the launch uses.
 struct W4Plan {
@@ -157,27 +167,38 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
                                       : gemv == FG_GEMV_WAVE  ? wave_fits
                                                               : (split_fits || tile_fits || wave_fits));
   const bool mfma_ok = !has_g_idx && q_aligned && x_aligned && (K % 8 == 0);
+  // the prefill kernel's shape conditions (an act-order perm, known only at launch, sends the call to MFMA instead)
+  const bool prefill_ok = mfma_ok && (K % 64 == 0) && (gs % 32 == 0 || G == 1);
   int use = impl;
-  if (use == FG_W4_AUTO) use = gemv_ok ? FG_W4_GEMV : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC);
+  if (use == FG_W4_AUTO)
+    use = gemv_ok ? FG_W4_GEMV : (prefill_ok && M >= kPrefillMinM ? FG_W4_PREFILL : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC));
+  if (use == FG_W4_PREFILL && !prefill_ok)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: prefill kernel needs K%%64==0, group%%32==0 (or one group), no g_idx, "
+                                 "ldq%%4==0, ldx%%8==0 and 16-byte aligned x/qweight");
   if (use == FG_W4_GEMV && !gemv_ok)
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: GEMV kernel %d needs M<=4, no g_idx, group%%32==0, ldq%%4==0, "
                                  "aligned qweight and a K / N it covers", gemv);
   if (use == FG_W4_MFMA && !mfma_ok)
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: MFMA path needs no g_idx, K%%8==0, ldq%%4==0, ldx%%8==0 and "
                                  "16-byte aligned x/qweight");
-  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC)
+  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC && use != FG_W4_PREFILL)
     return fail(FG_EINVAL, "fg_w4a16_gemm: unknown impl %d", impl);
   *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0};
   if (use == FG_W4_GEMV) {
     p->rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 4;
     if (p->rows != 1 && p->rows != 2 && p->rows != 4) return fail(FG_EINVAL, "fg_w4a16_gemm: rows_per_wave must be 1, 2 or 4");
     p->max_blocks = cfg ? cfg->max_blocks : 0;
-  } else if (use == FG_W4_MFMA) {
+  } else if (use == FG_W4_MFMA || use == FG_W4_PREFILL) {
     p->tile_m = cfg ? cfg->tile_m : 0;
     int kchunk = 0, used = 1;
     fg::w4_mfma_split_plan((int)M, (int)N, (int)K, p->tile_m, cfg ? cfg->split_k : 0, &kchunk, &used);
     p->splits = cfg && cfg->split_k ? cfg->split_k : 0;
     p->ws_bytes = used > 1 ? (size_t)used * (size_t)M * (size_t)N * sizeof(float) : 0;
+    // a prefill call falls back to the MFMA kernel under an act-order perm: size the workspace for either
+    if (use == FG_W4_PREFILL) {
+      const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits);
+      if (wb > p->ws_bytes) p->ws_bytes = wb;
+    }
   }
   return FG_OK;
 }
@@ -246,7 +267,10 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   } else if (p.impl == FG_W4_GEMV) {
     e = fg::launch_w4_gemv(p.mt, p.rows, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
                            bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, p.max_blocks, s);
-  } else if (p.impl == FG_W4_MFMA) {
+  } else if (p.impl == FG_W4_PREFILL && fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G)) {
+    e = fg::launch_w4_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y, ldy,
+                          static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
+  } else if (p.impl == FG_W4_MFMA || p.impl == FG_W4_PREFILL) {
     e = fg::launch_w4_mfma(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias, bias_dtype,
                            y, ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, p.tile_m, p.splits, s);
   } else {

@@ -172,4 +172,14 @@ __device__ __forceinline__ uint4 load16_stream(const void* p) {
 // nibble j (bits 4j..4j+3) of a packed word
 __device__ __forceinline__ uint32_t nibble(uint32_t w, int j) { return (w >> (4 * j)) & 0xFu; }
 
+__device__ __forceinline__ float raw_bits_to_f32(uint32_t raw, int dt) {
+  return dt == FG_F32 ? __builtin_bit_cast(float, raw)
+                      : (dt == FG_BF16 ? bf16_bits_to_f32(raw) : f16_bits_to_f32((uint16_t)raw));
+}
+
+// Element i of a 16- or 32-bit float array as raw bits (converted after the wait by raw_bits_to_f32).
+__device__ __forceinline__ uint32_t load_raw(const void* p, int dt, int64_t i) {
+  return dt == FG_F32 ? static_cast<const uint32_t*>(p)[i] : (uint32_t) static_cast<const uint16_t*>(p)[i];
+}
+
 }  // namespace fg

@@ -197,16 +197,6 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float raw_bits_to_f32(uint32_t raw, int dt) {
-  return dt == FG_F32 ? __builtin_bit_cast(float, raw)
-                      : (dt == FG_BF16 ? bf16_bits_to_f32(raw) : f16_bits_to_f32((uint16_t)raw));
-}
-
-// Element i of a 16- or 32-bit float array as raw bits (converted after the wait by raw_bits_to_f32).
-__device__ __forceinline__ uint32_t load_raw(const void* p, int dt, int64_t i) {
-  return dt == FG_F32 ? static_cast<const uint32_t*>(p)[i] : (uint32_t) static_cast<const uint16_t*>(p)[i];
-}
-
 // Stage everything a tile of TN channels [tile0, tile0+TN) reads besides qweight into LDS:
 //   xq[(m*4 + i) * KC + c] = word 4c+i of x row m as 16-bit pairs (x0,x2) (x1,x3) (x4,x6) (x5,x7), the order in
 //                            which the byte-permute unpack produces nibble pairs;  xs[m*KC + c] = fp32 sum of chunk c;

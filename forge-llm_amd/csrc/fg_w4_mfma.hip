@@ -200,6 +200,19 @@ __global__ void __launch_bounds__(256) w4_splitk_reduce_kernel(const float* __re
   y[(int64_t)m * ldy + n] = XBF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
 }
 
+template <bool XBF16>
+hipError_t launch_w4_splitk_reduce(const float* ws, int S, int M, int N, const void* bias, int bdt, void* y,
+                                   int64_t ldy, hipStream_t s) {
+  const int64_t MN = (int64_t)M * N;
+  hipLaunchKernelGGL(w4_splitk_reduce_kernel<XBF16>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s, ws, S, M, N,
+                     bias, bdt, static_cast<uint16_t*>(y), ldy);
+  return hipGetLastError();
+}
+template hipError_t launch_w4_splitk_reduce<true>(const float*, int, int, int, const void*, int, void*, int64_t,
+                                                  hipStream_t);
+template hipError_t launch_w4_splitk_reduce<false>(const float*, int, int, int, const void*, int, void*, int64_t,
+                                                   hipStream_t);
+
 // Tile shape per M bucket (wave grid WM x WN, wave tile (16 TM) x (16 TN)).
 struct W4Tile {
   int bm, bn;
@@ -248,10 +261,7 @@ static hipError_t launch_w4_mfma_t(const void* x, int64_t ldx, const int32_t* qw
                      scales, sdt, lds, zeros, ldz, bias, bdt, static_cast<uint16_t*>(y), ldy, ws, M, N, K, gs, kchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || used == 1) return e;
-  const int64_t MN = (int64_t)M * N;
-  hipLaunchKernelGGL(w4_splitk_reduce_kernel<XBF16>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s, ws, used, M,
-                     N, bias, bdt, static_cast<uint16_t*>(y), ldy);
-  return hipGetLastError();
+  return launch_w4_splitk_reduce<XBF16>(ws, used, M, N, bias, bdt, y, ldy, s);
 }
 
 template <bool XBF16>

@@ -133,12 +133,12 @@ def prepare_w4(packed: PackedW4) -> PackedW4:
     return p
 
 
-_IMPL_ALIASES = {"gemv": "gemv", "dot": "mfma", "mfma": "mfma", "dequant_matmul": "mfma", "legacy": "generic",
-                 "generic": "generic", "auto": None, None: None}
+_IMPL_ALIASES = {"gemv": "gemv", "dot": "mfma", "mfma": "mfma", "dequant_matmul": "mfma", "prefill": "prefill",
+                 "legacy": "generic", "generic": "generic", "auto": None, None: None}
 
 
 def forced_impl() -> str | None:
-    """``FORGE_W4_IMPL`` = gemv | mfma | generic (reference names dot / dequant_matmul / legacy are accepted)."""
+    """``FORGE_W4_IMPL`` = gemv | mfma | prefill | generic (reference names dot / dequant_matmul / legacy are accepted)."""
     v = os.environ.get("FORGE_W4_IMPL", "").strip().lower()
     return _IMPL_ALIASES.get(v) if v in _IMPL_ALIASES else None
 
@@ -149,7 +149,7 @@ def _w4_config(config: dict[str, Any] | None) -> _lib.W4Config | None:
         return None
     c = config or {}
     if c.get("impl") not in _IMPL_ALIASES:
-        raise ConfigError(f"unknown W4A16 impl {c.get('impl')!r}; choose gemv, mfma or generic")
+        raise ConfigError(f"unknown W4A16 impl {c.get('impl')!r}; choose gemv, mfma, prefill or generic")
     if c.get("gemv_kernel") not in _lib.GEMV_KERNEL:
         raise ConfigError(f"unknown GEMV kernel {c.get('gemv_kernel')!r}; choose split, tile or wave")
     return _lib.W4Config(_lib.W4_IMPL[impl], int(c.get("rows_per_wave") or 0), int(c.get("max_blocks") or 0),

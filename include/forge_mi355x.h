@@ -34,7 +34,9 @@ enum {
 enum { FG_OK = 0, FG_EINVAL = 1, FG_EUNSUPPORTED = 2, FG_EHIP = 3 };
 
 /* W4A16 implementation selector (fg_w4_config.impl) */
-enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3 };
+enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_PREFILL = 4 };
+/* FG_W4_PREFILL: 128/256 x 256 tiles, x straight to LDS, weights dequantised to LDS (large M x N; needs K % 64 == 0,
+   group % 32 == 0 or one group, aligned x / qweight, no act-order perm) */
 
 /* GEMV kernel selector (fg_w4_config.gemv_kernel) */
 enum { FG_GEMV_AUTO = 0, FG_GEMV_SPLIT = 1, FG_GEMV_TILE = 2, FG_GEMV_WAVE = 3 };

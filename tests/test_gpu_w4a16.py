@@ -107,6 +107,53 @@ def test_split_gemv_limits_and_unaligned_x():
                  what="unaligned x")
 
 
+@pytest.mark.parametrize("m,n,k,gs,sym,xdt,sdt", [
+    (128, 256, 256, 128, False, torch.bfloat16, torch.float16),
+    (300, 777, 1024, 32, True, torch.float16, torch.bfloat16),    # ragged M and N
+    (257, 1030, 640, -1, False, torch.bfloat16, torch.float32),     # one group, K not a multiple of 128
+    (512, 4096, 4096, 128, False, torch.bfloat16, torch.float16),   # 256-row tiles
+    (600, 2048, 2048, 64, True, torch.float16, torch.float16),
+])
+def test_prefill_kernel_matches_oracle(m, n, k, gs, sym, xdt, sdt):
+    y, ref = _case(m, n, k, gs, sym, xdt, bias=True, seed=m + k, scale_dtype=sdt, config={"impl": "prefill"})
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"prefill m={m} n={n} k={k} gs={gs}")
+
+
+@pytest.mark.parametrize("split_k", [2, 3])
+def test_prefill_split_k_and_reproducible(split_k):
+    q, s, z = w4_parts(1024, 2048, 128, False, seed=51)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(200, 2048, seed=52)
+    b = (torch.randn(1024, generator=gen(53)) * 0.5).bfloat16()
+    runs = [ops.w4a16_linear(x.to(DEV), p, b.to(DEV), config={"impl": "prefill", "split_k": split_k}) for _ in range(3)]
+    assert all(torch.equal(runs[0], r) for r in runs[1:])
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, 128), to_f32(b))
+    assert_close(runs[0].cpu(), ref, "bfloat16", what=f"prefill split {split_k}")
+
+
+def test_prefill_rejects_unsupported_and_policy_falls_back():
+    q, s, z = w4_parts(256, 1000, 8, False, seed=54)  # K % 64 != 0 and group 8
+    p = L.pack_w4(q, s, z, 8).to(DEV)
+    x = x_act(256, 1000, seed=55)
+    with pytest.raises(ForgeError):
+        ops.w4a16_linear(x.to(DEV), p, config={"impl": "prefill"})
+    y = ops.w4a16_linear(x.to(DEV), p)
+    assert_close(y.cpu(), og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, 8)), "bfloat16", what="fallback")
+
+
+@pytest.mark.parametrize("m,kn", [(2048, (4096, 28672)), (8192, (14336, 4096))])
+def test_prefill_full_size_llama_shapes(m, kn):
+    """configs[2] shapes at full size; the oracle checks 48 spread rows (the full fp32 GEMM is too slow on the CPU)."""
+    k, n = kn
+    q, s, z = w4_parts(n, k, 128, False, seed=m)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(m, k, seed=m + 1)
+    y = ops.w4a16_linear(x.to(DEV), p).cpu()
+    rows = torch.linspace(0, m - 1, 48).long()
+    ref = og.w4a16_gemm_ref(to_f32(x[rows]), oracle_packed(q, s, z, 128))
+    assert_close(y[rows], ref, "bfloat16", what=f"prefill M={m} K={k} N={n}")
+
+
 @pytest.mark.parametrize("m", [5, 16, 33, 64, 256])
 @pytest.mark.parametrize("n,k", [(4096, 4096), (777, 2048)])
 @pytest.mark.parametrize("gs", [128, 32])

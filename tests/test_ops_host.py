@@ -70,6 +70,7 @@ def test_prepare_fp8_scales_rejects_mismatches():
 def test_w4_config_aliases(monkeypatch):
     assert ops._w4_config(None) is None
     assert ops._w4_config({"impl": "dot"}).impl == 2 and ops._w4_config({"impl": "legacy"}).impl == 3
+    assert ops._w4_config({"impl": "prefill"}).impl == 4
     assert ops._w4_config({"impl": "gemv", "rows_per_wave": 2}).rows_per_wave == 2
     assert ops._w4_config({"impl": "gemv", "gemv_kernel": "tile"}).gemv_kernel == 2
     assert ops._w4_config({"impl": "gemv"}).gemv_kernel == 0
