@@ -29,6 +29,12 @@ void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchun
 bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
                int64_t G);
 size_t w4_big_workspace_bytes(int M, int N, int K, int split_k);
+bool w4_skinny_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int sdt,
+                  int64_t lds, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
+hipError_t launch_w4_skinny(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
+                            const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
+                            const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
+                            bool single_group, hipStream_t s);
 hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
                          int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
@@ -270,6 +276,11 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   } else if (p.impl == FG_W4_PREFILL && fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G)) {
     e = fg::launch_w4_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y, ldy,
                           static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
+  } else if (p.impl == FG_W4_MFMA && !(cfg && (cfg->tile_m || cfg->split_k)) && !(M > 32 && N >= 16384) &&
+             fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G)) {
+    // (the LDS-tiled kernel measured faster for 33..64 rows over wide outputs: 593 against 485 GB/s on gate+up)
+    e = fg::launch_w4_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
+                             ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (p.impl == FG_W4_MFMA || p.impl == FG_W4_PREFILL) {
     e = fg::launch_w4_mfma(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias, bias_dtype,
                            y, ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, p.tile_m, p.splits, s);

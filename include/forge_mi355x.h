@@ -46,8 +46,9 @@ typedef struct fg_w4_config {
   int32_t impl;         /* FG_W4_* */
   int32_t rows_per_wave; /* GEMV: output channels per wavefront (1, 2 or 4) */
   int32_t max_blocks;   /* GEMV: cap on workgroups (grid-stride beyond it) */
-  int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128) */
-  int32_t split_k;      /* MFMA: K splits (fp32 partials in the workspace, reduced in fixed order) */
+  int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128); setting it (or split_k) selects
+                           the LDS-tiled MFMA kernel over the register-resident split-K kernel used for M <= 64 */
+  int32_t split_k;      /* MFMA / PREFILL: K splits (fp32 partials in the workspace, reduced in fixed order) */
   int32_t tile_n;       /* GEMV tile kernel: output channels per workgroup tile (rounded up to a multiple of 8) */
   int32_t gemv_kernel;  /* GEMV: FG_GEMV_SPLIT = split-K register kernel (M <= 4, K <= 65536), FG_GEMV_TILE = LDS-tiled
                            kernel, FG_GEMV_WAVE = one-wavefront-per-row-block kernel; AUTO = split when it fits,
