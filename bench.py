@@ -10,6 +10,7 @@ value = algorithmic bytes per step / step time, bytes per linear = N*K/2 + 2*G*N
 
 Secondary (``w4_decode_sweep``, ``w4_prefill``): the same four shapes at M in {4, 16, 64} (configs[1], GB/s) and
 M in {512, 2048, 8192} (configs[2], TFLOP/s against 2.5 PFLOP/s dense bf16).
+Secondary (``w8a8_small_m``): FP8 at M in {16, 256} and INT8 at M in {1, 64} (HBM-bound, GB/s).
 Secondary (``w8a8``): FP8 e4m3fn GEMM at M=4096, K=N=8192 and INT8 GEMM at M=4096 on the Llama-3-70B
 shapes, in TFLOP/s against the dense fp8 / int8 MFMA peaks, on pre-quantised operands.
 
@@ -137,6 +138,51 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
         prefill[f"M{m}"] = row
         log(f"prefill M={m}: " + "  ".join(f"{nm} {v['ms']:.3f} ms {v['tflops']:.0f} TF" for nm, v in row.items()))
     return decode, prefill
+
+
+def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
+    """configs[3] fp8 at M in {16, 256} (K = N = 8192) and configs[4] int8 at M in {1, 64} on the three 70B shapes:
+    HBM-bound, reported in GB/s of algorithmic bytes (weights N*K + activations M*K + scales + bf16 output) and in
+    TFLOP/s."""
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(11)
+    k, n = 8192, 8192
+    ring = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.float8_e4m3fn) for _ in range(6)]
+    sw = torch.rand(n, device=dev, generator=gen) * 0.01
+    for m in (16, 256):
+        xq = torch.randn(m, k, device=dev, generator=gen).to(torch.float8_e4m3fn)
+        sx = torch.rand(m, device=dev, generator=gen) * 0.01
+
+        def run(xq=xq, sx=sx):
+            for w in ring:
+                ops.fp8_linear(xq, w, sw, x_scale=sx, out_dtype=torch.bfloat16)
+
+        ms = time_eager(torch, run, reps, 3) / len(ring)
+        by = n * k + m * k + 4 * (m + n) + 2 * m * n
+        out[f"fp8_m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
+                                      "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+        log(f"fp8 M={m} K=N=8192: {ms * 1e3:.1f} us  {out[f'fp8_m{m}_k{k}_n{n}']['GBps']:.0f} GB/s")
+    del ring
+    for (k8, n8) in ((8192, 10240), (8192, 57344), (28672, 8192)):
+        nring = max(2, min(6, (1536 << 20) // (n8 * k8)))
+        ring = [torch.randint(-127, 128, (n8, k8), dtype=torch.int8, device=dev, generator=gen) for _ in range(nring)]
+        swi = torch.rand(n8, device=dev, generator=gen) * 0.01
+        for m in (1, 64):
+            xi = torch.randint(-127, 128, (m, k8), dtype=torch.int8, device=dev, generator=gen)
+            sxi = torch.rand(m, device=dev, generator=gen) * 0.01
+
+            def run(xi=xi, sxi=sxi):
+                for w in ring:
+                    ops.int8_linear(xi, w, swi, x_scale=sxi, out_dtype=torch.bfloat16)
+
+            ms = time_eager(torch, run, reps, 3) / len(ring)
+            by = n8 * k8 + m * k8 + 4 * (m + n8) + 2 * m * n8
+            key = f"int8_m{m}_k{k8}_n{n8}"
+            out[key] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            log(f"int8 M={m} K={k8} N={n8}: {ms * 1e3:.1f} us  {out[key]['GBps']:.0f} GB/s")
+        del ring
+    return out
 
 
 def bench_w8a8(torch, ops, dev, reps: int) -> dict:
@@ -315,6 +361,8 @@ def main() -> None:
     torch.cuda.empty_cache()
     if not args.no_w8a8:
         out["w8a8"] = bench_w8a8(torch, ops, dev, max(5, args.steps))
+        if not args.no_sweep:
+            out["w8a8_small_m"] = bench_w8a8_small(torch, ops, dev, max(5, args.steps))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

@@ -60,6 +60,13 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64
                            int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
                            int64_t ldy, int ydt, int M, int N, int K, int tile, hipStream_t s);
 bool mm_big_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t K);
+bool w8_skinny_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N, int64_t K);
+hipError_t launch_int8_gemm_skinny(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                                   int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                                   int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
+hipError_t launch_fp8_gemm_skinny(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
+                                  int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
+                                  int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
 int64_t mm_big_tiles(int64_t M, int64_t N);
 hipError_t launch_int8_gemm_big(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                                 int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
@@ -107,12 +114,21 @@ constexpr int64_t kMaxDim = (int64_t)1 << 31;
 // W8A8 tile policy: tile_m = 256 (config or automatic) selects the 256 x 256 direct-to-LDS kernel, which needs
 // K % 128 == 0 and 16-byte aligned operands with 16-byte multiple leading dimensions; it is chosen automatically once
 // its tiles cover every CU of an MI355X (256) at least once.  Otherwise 64 x 64 (M or N <= 64) or 128 x 128 tiles.
+// Tile 16 selects the skinny kernel (M <= 64, K % 256 == 0, 16-byte aligned operands; register-resident split-K),
+// chosen automatically for M <= 64 where it applies.
 int mm_tile(int64_t M, int64_t N, int64_t K, const void* a, int64_t lda, const void* b, int64_t ldb,
             const fg_mm_config* cfg) {
   const bool big_ok = fg::mm_big_ok(a, lda, b, ldb, K);
-  if (cfg && cfg->tile_m) return (cfg->tile_m == 256 && !big_ok) ? -1 : cfg->tile_m;
+  const bool skinny_ok = fg::w8_skinny_ok(a, lda, b, ldb, M, N, K);
+  if (cfg && cfg->tile_m)
+    return ((cfg->tile_m == 256 && !big_ok) || (cfg->tile_m == 16 && !skinny_ok)) ? -1 : cfg->tile_m;
+  // measured on the configs' shapes: the skinny kernel wins for M <= 16 below N = 32768 and for M <= 64 below
+  // N = 16384; 64-row tiles win while 128-row tiles would leave fewer than two per CU (fp8 M = 256: 538 against
+  // 381 TFLOP/s)
+  if (skinny_ok && N < 32768 && (M <= 16 || N < 16384)) return 16;
   if (big_ok && fg::mm_big_tiles(M, N) >= 256) return 256;
-  return (M <= 64 || N <= 64) ? 64 : 128;
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+  return (M <= 64 || N <= 64 || tiles128 < 512) ? 64 : 128;
 }
 
 }  // namespace
@@ -325,7 +341,12 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
   const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
   if (tile < 0)
-    return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0 and 16-byte aligned operands");
+    return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
+                                 "both 16-byte aligned operands");
+  if (tile == 16)
+    return hip_status(fg::launch_int8_gemm_skinny(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy,
+                                                  y_dtype, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream)),
+                      "fg_int8_gemm launch");
   if (tile == 256)
     return hip_status(fg::launch_int8_gemm_big(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy,
                                                y_dtype, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream)),
@@ -351,7 +372,12 @@ int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, i
     if (scale_mode == 0) sa_sm = sb_sn = 0;
     const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
     if (tile < 0)
-      return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0 and 16-byte aligned operands");
+      return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
+                                   "both 16-byte aligned operands");
+    if (tile == 16)
+      return hip_status(fg::launch_fp8_gemm_skinny(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy,
+                                                   y_dtype, (int)M, (int)N, (int)K, s),
+                        "fg_fp8_gemm launch");
     if (tile == 256)
       return hip_status(fg::launch_fp8_gemm_big(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy, y_dtype,
                                                 (int)M, (int)N, (int)K, s),
