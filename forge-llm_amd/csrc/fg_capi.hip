@@ -157,8 +157,10 @@ int fg_device_ok(int device) {
 
 namespace {
 
-// Rows of x from which the policy takes the prefill kernel over the skinny MFMA kernel.
-constexpr int64_t kPrefillMinM = 128;
+// Rows of x from which the policy takes the prefill kernel (64/128/256-row tiles, split-K) over the skinny MFMA
+// kernel: measured on the Llama-3-8B shapes, the skinny kernel wins up to 32 rows (and to 64 rows for N, K <= 4096),
+// the prefill kernel from 48 rows (gate+up at M = 64: 1.10 against 0.60 TB/s).
+constexpr int64_t kPrefillMinM = 33;
 
 // Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
 // workspace a caller sizes is the workspace the launch uses.
@@ -216,8 +218,9 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
     fg::w4_mfma_split_plan((int)M, (int)N, (int)K, p->tile_m, cfg ? cfg->split_k : 0, &kchunk, &used);
     p->splits = cfg && cfg->split_k ? cfg->split_k : 0;
     p->ws_bytes = used > 1 ? (size_t)used * (size_t)M * (size_t)N * sizeof(float) : 0;
-    // a prefill call falls back to the MFMA kernel under an act-order perm: size the workspace for either
-    if (use == FG_W4_PREFILL) {
+    // the launch picks among the skinny, prefill and tiled MFMA kernels once the operand addresses are known (an
+    // act-order perm or misaligned operands rule some out): size the workspace for either split-K kernel
+    if (prefill_ok) {
       const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits);
       if (wb > p->ws_bytes) p->ws_bytes = wb;
     }
@@ -289,17 +292,27 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   } else if (p.impl == FG_W4_GEMV) {
     e = fg::launch_w4_gemv(p.mt, p.rows, xbf16, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
                            bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, p.max_blocks, s);
-  } else if (p.impl == FG_W4_PREFILL && fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G)) {
-    e = fg::launch_w4_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y, ldy,
-                          static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
-  } else if (p.impl == FG_W4_MFMA && !(cfg && (cfg->tile_m || cfg->split_k)) && !(M > 32 && N >= 16384) &&
-             fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G)) {
-    // (the LDS-tiled kernel measured faster for 33..64 rows over wide outputs: 593 against 485 GB/s on gate+up)
-    e = fg::launch_w4_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
-                             ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (p.impl == FG_W4_MFMA || p.impl == FG_W4_PREFILL) {
-    e = fg::launch_w4_mfma(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias, bias_dtype,
-                           y, ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, p.tile_m, p.splits, s);
+    const bool auto_impl = !cfg || cfg->impl == FG_W4_AUTO;
+    const bool skinny = !(cfg && (cfg->tile_m || cfg->split_k)) &&
+                        fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K,
+                                         gs, G);
+    const bool big = fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G) && !(cfg && cfg->tile_m);
+    int kern = 0;  // 0: LDS-tiled MFMA, 1: skinny, 2: prefill
+    if (p.impl == FG_W4_PREFILL)
+      kern = (auto_impl && skinny && M <= 64 && N <= 4096 && K <= 4096) ? 1 : (big ? 2 : 0);
+    else
+      kern = skinny ? 1 : ((auto_impl && big) ? 2 : 0);
+    if (kern == 1)
+      e = fg::launch_w4_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
+                               ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
+    else if (kern == 2)
+      e = fg::launch_w4_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
+                            ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
+    else
+      e = fg::launch_w4_mfma(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, bias,
+                             bias_dtype, y, ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, p.tile_m,
+                             p.splits, s);
   } else {
     e = fg::launch_w4_generic(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias,
                               bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, s);

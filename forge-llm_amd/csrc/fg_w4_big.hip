@@ -1,6 +1,7 @@
 // W4A16 prefill on matrix cores for large M x N: y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+bias).
 //
-// Workgroup tile BM x 256 (BM = 256 or 128), 512 threads = 2 x 4 wavefronts of (BM/2) x 64, 16 x 16 output tiles of
+// Workgroup tile BM x 256 (BM = 256, 128 or 64), 512 threads = 2 x 4 wavefronts of (BM/2) x 64 (BM = 64: 1 x 8
+// wavefronts of 64 x 32), 16 x 16 output tiles of
 // v_mfma_f32_16x16x32_{bf16,f16}.  K is walked in 64-column slices (128 bytes of x per row) through a double-buffered
 // LDS ring:
 //   * x: written straight from global memory into LDS by global_load_lds_dwordx4 (no registers, no VALU), one
@@ -67,7 +68,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz, int hasz,
     const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ ws, int M,
     int N, int K, int gs32, int kchunk) {
-  constexpr int BN = kW4BigBN, BK = kW4BigBK, NT = kW4BigThreads, WM = 2, WN = 4;
+  constexpr int BN = kW4BigBN, BK = kW4BigBK, NT = kW4BigThreads, WM = BM >= 128 ? 2 : 1, WN = 8 / WM;
   constexpr int ROW = BK * 2;                  // bytes per LDS row
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int X_INSTR = BM * ROW / 16 / NT;  // 1 KiB x load instructions per wavefront and slice
@@ -231,14 +232,15 @@ bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const
          (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0;
 }
 
-// Row tile (256 or 128) and K splits: 256 x 256 tiles when they alone cover the CUs, else 128 x 256 tiles, split over
-// K (in 64-column slices, at least 512 columns each) until about one workgroup per CU exists.
+// Row tile and K splits: 256 x 256 tiles when they alone cover the CUs, 64 x 256 for M <= 64, else 128 x 256, split
+// over K (in 64-column slices, at least 512 columns each) until about one workgroup per CU exists.
 void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kchunk) {
   const int cus = 256;
   const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + kW4BigBN - 1) / kW4BigBN);
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + kW4BigBN - 1) / kW4BigBN);
-  *bm = t256 >= cus ? 256 : 128;
-  const int64_t tiles = *bm == 256 ? t256 : t128;
+  const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + kW4BigBN - 1) / kW4BigBN);
+  *bm = t256 >= cus ? 256 : (M <= 64 ? 64 : 128);
+  const int64_t tiles = *bm == 256 ? t256 : (*bm == 128 ? t128 : t64);
   int s = split_k;
   if (s <= 0) {
     s = tiles >= cus ? 1 : (int)((cus + tiles - 1) / tiles);
@@ -296,9 +298,11 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
                                    gs32, splits, kchunk, s)
   if (xbf16) {
     if (bm == 256) FG_W4BIG(256, true);
+    if (bm == 64) FG_W4BIG(64, true);
     FG_W4BIG(128, true);
   }
   if (bm == 256) FG_W4BIG(256, false);
+  if (bm == 64) FG_W4BIG(64, false);
   FG_W4BIG(128, false);
 #undef FG_W4BIG
 }
