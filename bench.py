@@ -10,6 +10,7 @@ value = algorithmic bytes per step / step time, bytes per linear = N*K/2 + 2*G*N
 
 Secondary (``w4_decode_sweep``, ``w4_prefill``): the same four shapes at M in {4, 16, 64} (configs[1], GB/s) and
 M in {512, 2048, 8192} (configs[2], TFLOP/s against 2.5 PFLOP/s dense bf16).
+Secondary (``w8a16_decode``): int8 weight-only linears on the same shapes at M in {1, 16} (GB/s).
 Secondary (``w8a8_small_m``): FP8 at M in {16, 256} and INT8 at M in {1, 64} (HBM-bound, GB/s).
 Secondary (``w8a8``): FP8 e4m3fn GEMM at M=4096, K=N=8192 and INT8 GEMM at M=4096 on the Llama-3-70B
 shapes, in TFLOP/s against the dense fp8 / int8 MFMA peaks, on pre-quantised operands.
@@ -138,6 +139,34 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
         prefill[f"M{m}"] = row
         log(f"prefill M={m}: " + "  ".join(f"{nm} {v['ms']:.3f} ms {v['tflops']:.0f} TF" for nm, v in row.items()))
     return decode, prefill
+
+
+def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -> dict:
+    """W8A16 (int8 weight-only, per-channel fp16 scales) decode on the four Llama-3-8B shapes at M in {1, 16}: HBM
+    GB/s of algorithmic bytes (N*K weights + 2*N scales + 2*M*K + 2*M*N), HIP-graph replays over a ring of distinct
+    weights (at least 1.2 GB per shape)."""
+    out = {}
+    for name, (k, n) in SHAPES.items():
+        nring = max(4, (1200 << 20) // (n * k) + 1)
+        ring = [layouts.PackedW8(torch.randint(-128, 128, (n, k), dtype=torch.int8, device=dev, generator=gen),
+                                 (torch.rand(1, n, device=dev, generator=gen) * 0.018 + 0.002).half(),
+                                 layouts.PORTABLE_W8, n, k, -1) for _ in range(nring)]
+        row = {}
+        for m in (1, 16):
+            x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+
+            def run(x=x, ring=ring):
+                for p in ring:
+                    ops.w8a16_linear(x, p)
+
+            t = timer(torch, run, steps, warmup) / len(ring)
+            by = n * k + 2 * n + 2 * m * (k + n)
+            row[f"M{m}"] = {"us": round(t * 1e3, 3), "GBps": round(by / (t * 1e-3) / 1e9, 1),
+                            "frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        out[name] = row
+        log(f"w8a16 {name:8s}: " + "  ".join(f"M={mm[1:]} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for mm, v in row.items()))
+        del ring
+    return out
 
 
 def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
@@ -359,6 +388,9 @@ def main() -> None:
                                                                    args.warmup)
     del ring
     torch.cuda.empty_cache()
+    if not args.no_sweep:
+        out["w8a16_decode"] = bench_w8a16(torch, layouts, ops, dev, gen, timer, args.steps, args.warmup)
+        torch.cuda.empty_cache()
     if not args.no_w8a8:
         out["w8a8"] = bench_w8a8(torch, ops, dev, max(5, args.steps))
         if not args.no_sweep:

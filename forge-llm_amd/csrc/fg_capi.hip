@@ -29,6 +29,18 @@ void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchun
 bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
                int64_t G);
 size_t w4_big_workspace_bytes(int M, int N, int K, int split_k);
+bool w8a16_skinny_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int sdt, int64_t lds, int64_t M,
+                     int64_t N, int64_t K, int gs, int64_t G);
+hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                               const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                               int64_t ldy, int M, int N, int K, int gs, bool single_group, hipStream_t s);
+hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq,
+                                const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                                int64_t ldy, int M, int N, int K, int gs, hipStream_t s);
+bool w8_big_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int64_t K, int gs, int64_t G);
+hipError_t launch_w8_big(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq, const void* scales,
+                         int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M,
+                         int N, int K, int gs, bool single_group, int split_k, hipStream_t s);
 bool w4_skinny_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int sdt,
                   int64_t lds, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
 hipError_t launch_w4_skinny(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
@@ -335,6 +347,67 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
   return hip_status(fg::launch_w4_dequant(qweight, ldq, scales, scale_dtype, lds, zeros, ldz, g_idx, out, out_dtype,
                                           ldo, (int)N, (int)K, gs, static_cast<hipStream_t>(stream)),
                     "fg_w4_dequant launch");
+}
+
+size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, const fg_w4_config* cfg) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int64_t G = (K + gs - 1) / gs;
+  const int impl = cfg ? cfg->impl : FG_W4_AUTO;
+  // the prefill kernel's split-K partials, whenever it may run (its alignment conditions are checked at launch)
+  const bool prefill_shape = (K % 64 == 0) && (gs % 32 == 0 || G == 1);
+  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA) return 0;
+  return fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0);
+}
+
+int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
+                  int scale_dtype, int64_t lds, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M,
+                  int64_t N, int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg,
+                  void* workspace, size_t workspace_bytes, fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_w8a16_gemm: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (M == 0) return FG_OK;
+  if (x_dtype != FG_BF16 && x_dtype != FG_F16) return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: x must be bf16 or fp16");
+  if (!is_float_dt(scale_dtype)) return fail(FG_EINVAL, "fg_w8a16_gemm: bad scale dtype %d", scale_dtype);
+  if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_w8a16_gemm: bad bias dtype %d", bias_dtype);
+  if (!x || !qweight || !scales || !y) return fail(FG_EINVAL, "fg_w8a16_gemm: null tensor");
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int64_t G = (K + gs - 1) / gs;
+  if (ldq < K || lds < N || ldx < K || ldy < N) return fail(FG_EINVAL, "fg_w8a16_gemm: leading dimensions too small");
+  if (n_groups < G)
+    return fail(FG_EINVAL, "fg_w8a16_gemm: n_groups=%d does not cover K=%lld with group %d", n_groups, (long long)K, gs);
+  const int impl = cfg ? cfg->impl : FG_W4_AUTO;
+  if (impl != FG_W4_AUTO && impl != FG_W4_MFMA && impl != FG_W4_PREFILL && impl != FG_W4_GENERIC)
+    return fail(FG_EINVAL, "fg_w8a16_gemm: unknown impl %d", impl);
+  const bool xbf16 = x_dtype == FG_BF16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);
+  const bool big = fg::w8_big_ok(x, ldx, qweight, ldq, K, gs, G);
+  int kern = impl == FG_W4_GENERIC ? 0 : (impl == FG_W4_MFMA ? 1 : (impl == FG_W4_PREFILL ? 2 : -1));
+  if (kern < 0) kern = (skinny && M <= 64) ? 1 : (big ? 2 : 0);
+  if (kern == 1 && !skinny)
+    return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: skinny kernel needs M<=64, K%%128==0, group%%128==0 (or one group), "
+                                 "16-bit scales, ldq%%16==0, ldx%%8==0 and 16-byte aligned x/qweight");
+  if (kern == 2 && !big)
+    return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: prefill kernel needs K%%64==0, group%%32==0 (or one group), "
+                                 "ldq%%16==0, ldx%%8==0 and 16-byte aligned x/qweight");
+  hipError_t e;
+  if (kern == 1) {
+    e = fg::launch_w8a16_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
+                                (int)M, (int)N, (int)K, gs, G == 1, s);
+  } else if (kern == 2) {
+    const size_t need = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(FG_EINVAL, "fg_w8a16_gemm: workspace of %zu bytes needed, %zu given", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    e = fg::launch_w8_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
+                          static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, cfg ? cfg->split_k : 0,
+                          s);
+  } else {
+    e = fg::launch_w8a16_generic(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
+                                 (int)M, (int)N, (int)K, gs, s);
+  }
+  return hip_status(e, "fg_w8a16_gemm launch");
 }
 
 int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b, int64_t ldb,

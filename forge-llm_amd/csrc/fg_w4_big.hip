@@ -62,9 +62,11 @@ __device__ __forceinline__ uint4 w4big_frag(const uint8_t* rp, int r16, int lane
   return *reinterpret_cast<const uint4*>(rp + c * 16);
 }
 
-template <int BM, bool XBF16>
+// WB = 4: packed int4 qweight (int32 words, ldq in words) with zero-points; WB = 8: int8 qweight (ldq in bytes),
+// symmetric (W8A16).
+template <int BM, bool XBF16, int WB>
 __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ qw, int64_t ldq,
+    const uint16_t* __restrict__ x, int64_t ldx, const void* __restrict__ qw, int64_t ldq,
     const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz, int hasz,
     const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ ws, int M,
     int N, int K, int gs32, int kchunk) {
@@ -99,23 +101,44 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
   // W: thread t owns row t / 2 of the tile, columns 32 (t % 2) .. + 32 of each slice (4 packed words)
   const int wrow = tid >> 1, whalf = tid & 1;
   const int wn_ = min(n0 + wrow, N - 1);
-  const uint4* __restrict__ wsrc = reinterpret_cast<const uint4*>(qw + (int64_t)wn_ * ldq) + whalf;
+  // this thread's 32 columns of each slice: 16 bytes of packed int4 or 32 bytes of int8
+  const uint4* __restrict__ wsrc =
+      WB == 4 ? reinterpret_cast<const uint4*>(static_cast<const int32_t*>(qw) + (int64_t)wn_ * ldq) + whalf
+              : reinterpret_cast<const uint4*>(static_cast<const int8_t*>(qw) + (int64_t)wn_ * ldq) + 2 * whalf;
   const FastDiv gdiv((uint32_t)max(gs32, 1));
-  uint4 wreg;
+  uint4 wreg, wreg2;
   uint32_t sreg, zreg;
   auto fetch_w = [&](int k0) __attribute__((always_inline)) {
     const int c = (k0 >> 5) + whalf;  // 32-column chunk index
     const int g = gs32 > 0 ? (int)gdiv.div((uint32_t)c) : 0;
-    wreg = load16_stream(wsrc + (k0 >> 5));
+    if constexpr (WB == 4) {
+      wreg = load16_stream(wsrc + (k0 >> 5));
+    } else {
+      wreg = load16_stream(wsrc + (k0 >> 4));
+      wreg2 = load16_stream(wsrc + (k0 >> 4) + 1);
+    }
     sreg = load_raw(scales, sdt, (int64_t)g * lds + wn_);
-    zreg = (uint32_t)zeros[(int64_t)g * ldz + (wn_ >> 3)];
+    if constexpr (WB == 4) zreg = (uint32_t)zeros[(int64_t)g * ldz + (wn_ >> 3)];
   };
   auto stash_w = [&](uint8_t* st) __attribute__((always_inline)) {
     const float s = raw_bits_to_f32(sreg, sdt);
+    uint8_t* rp = st + BM * ROW + wrow * ROW;
+    if constexpr (WB == 8) {  // 32 signed bytes: q * s exactly as the oracle's fp32 product, rounded once
+      const uint32_t wd[8] = {wreg.x, wreg.y, wreg.z, wreg.w, wreg2.x, wreg2.y, wreg2.z, wreg2.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float d[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) d[b] = (float)(int8_t)(wd[2 * i + b / 4] >> (8 * (b % 4))) * s;
+        const uint4 v = make_uint4(w4big_pack<XBF16>(d[0], d[1]), w4big_pack<XBF16>(d[2], d[3]),
+                                   w4big_pack<XBF16>(d[4], d[5]), w4big_pack<XBF16>(d[6], d[7]));
+        *reinterpret_cast<uint4*>(rp + (((4 * whalf + i) ^ (wrow & 7)) * 16)) = v;
+      }
+      return;
+    }
     const float z = hasz ? (float)nibble(zreg, wn_ & 7) : 8.f;
     const float c = -z * s;
     const uint32_t wd[4] = {wreg.x, wreg.y, wreg.z, wreg.w};
-    uint8_t* rp = st + BM * ROW + wrow * ROW;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // word i = columns 8 i .. 8 i + 7 of this thread's 32 = LDS unit 4 whalf + i
       const uint32_t lo = wd[i] & 0x0F0F0F0Fu, hi = (wd[i] >> 4) & 0x0F0F0F0Fu;  // nibbles 0,2,4,6 / 1,3,5,7
@@ -264,18 +287,18 @@ template <bool XBF16>
 hipError_t launch_w4_splitk_reduce(const float* ws, int S, int M, int N, const void* bias, int bdt, void* y,
                                    int64_t ldy, hipStream_t s);
 
-template <int BM, bool XBF16>
-static hipError_t launch_w4_big_t(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales,
+template <int BM, bool XBF16, int WB>
+static hipError_t launch_w4_big_t(const void* x, int64_t ldx, const void* qw, int64_t ldq, const void* scales,
                                   int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt,
                                   void* y, int64_t ldy, float* ws, int M, int N, int K, int gs32, int splits,
                                   int kchunk, hipStream_t s) {
   constexpr size_t shm = 2 * (size_t)(BM + kW4BigBN) * kW4BigBK * 2;
-  auto kern = w4_big_kernel<BM, XBF16>;
+  auto kern = w4_big_kernel<BM, XBF16, WB>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)shm);
   if (e != hipSuccess) return e;
   const int hasz = zeros != nullptr;
-  const int32_t* zp = hasz ? zeros : qw;  // symmetric: a valid dummy word, ignored
+  const int32_t* zp = hasz ? zeros : static_cast<const int32_t*>(qw);  // symmetric: a valid dummy word, ignored
   const int64_t ldzp = hasz ? ldz : 0;
   const int tiles = ((M + BM - 1) / BM) * ((N + kW4BigBN - 1) / kW4BigBN);
   hipLaunchKernelGGL(kern, dim3(tiles, splits), dim3(kW4BigThreads), shm, s, static_cast<const uint16_t*>(x), ldx, qw,
@@ -293,9 +316,9 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
   int bm, splits, kchunk;
   w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk);
   const int gs32 = single_group ? 0 : gs / 32;
-#define FG_W4BIG(BM_, XB_)                                                                                          \
-  return launch_w4_big_t<BM_, XB_>(x, ldx, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy, ws, M, N, K, \
-                                   gs32, splits, kchunk, s)
+#define FG_W4BIG(BM_, XB_)                                                                                             \
+  return launch_w4_big_t<BM_, XB_, 4>(x, ldx, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy, ws, M, N, K, \
+                                      gs32, splits, kchunk, s)
   if (xbf16) {
     if (bm == 256) FG_W4BIG(256, true);
     if (bm == 64) FG_W4BIG(64, true);
@@ -305,6 +328,32 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
   if (bm == 64) FG_W4BIG(64, false);
   FG_W4BIG(128, false);
 #undef FG_W4BIG
+}
+
+// W8A16 through the same kernel (int8 qweight, ldq in bytes, no zero-points).
+bool w8_big_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int64_t K, int gs, int64_t G) {
+  return (K % kW4BigBK) == 0 && ((gs % 32) == 0 || G == 1) && (ldx % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0;
+}
+
+hipError_t launch_w8_big(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq, const void* scales,
+                         int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M,
+                         int N, int K, int gs, bool single_group, int split_k, hipStream_t s) {
+  int bm, splits, kchunk;
+  w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk);
+  const int gs32 = single_group ? 0 : gs / 32;
+#define FG_W8BIG(BM_, XB_)                                                                                         \
+  return launch_w4_big_t<BM_, XB_, 8>(x, ldx, qw, ldq, scales, sdt, lds, nullptr, 0, bias, bdt, y, ldy, ws, M, N, \
+                                      K, gs32, splits, kchunk, s)
+  if (xbf16) {
+    if (bm == 256) FG_W8BIG(256, true);
+    if (bm == 64) FG_W8BIG(64, true);
+    FG_W8BIG(128, true);
+  }
+  if (bm == 256) FG_W8BIG(256, false);
+  if (bm == 64) FG_W8BIG(64, false);
+  FG_W8BIG(128, false);
+#undef FG_W8BIG
 }
 
 }  // namespace fg

@@ -1,0 +1,327 @@
+// W8A16 (int8 weight-only): y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+bias), W[n,k] = q[n,k] * s[g(k), n], q signed int8
+// (symmetric, no zero-point), x bf16 / fp16.  The portable_row W8 layout: qweight int8 [N, K] row-major, scales [G, N].
+//
+// Skinny kernel (M <= 64): the W4 skinny kernel's split-K structure (a wavefront owns T tiles of 16 channels and one K
+// slice in 128-column steps; KS slices per workgroup summed in slice order through LDS; operands straight from global
+// memory into registers by raw buffer loads, two steps ahead).  Lane l (row l % 16, lane group j = l / 16) loads the
+// 32 weight bytes 32 j .. 32 j + 31 of its row per step and the 64 bytes of x over the same columns; MFMA k-step s
+// takes weight bytes 8 s .. 8 s + 7 and x columns 32 j + 8 s .. + 7 in natural order.  The signed byte q becomes
+// u = q ^ 0x80 = q + 128 (0..255):
+//   fp16 x: one exact fp16 per byte, 0x6400 | u = 1024 + u (byte-permutes against the magic exponent byte), one MFMA
+//           per k-step:  sum x q = A - 1152 sum x;
+//   bf16 x: bf16 holds 128 + v exactly only for v < 128, so u splits into nibble planes h = u >> 4 and l = u & 15,
+//           each 128 + v through the magic byte, two MFMAs per k-step:  sum x q = 16 A_h + A_l - 2304 sum x.
+// The row sums of x come from one MFMA per k-step against all-ones (in the accumulator layout); each step lies in one
+// group (group size a multiple of 128, or one group), so after a step  acc += s[n, g] * (that expression).
+//
+// Generic kernel: any shape, stride, alignment, group size and scale dtype; one wavefront per output channel and up
+// to 4 rows of x, lanes stride over K, fp32 products q * s * x in the oracle's order of dequantise-then-multiply.
+#include "fg_device.h"
+
+namespace fg {
+
+typedef __bf16 bf16x8_w8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_w8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_w8_t __attribute__((ext_vector_type(4)));
+
+template <bool XBF16>
+__device__ __forceinline__ f32x4_w8_t w8_mfma(uint4 a, uint4 b, f32x4_w8_t c) {
+  if constexpr (XBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_w8_t, a),
+                                                   __builtin_bit_cast(bf16x8_w8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_w8_t, a),
+                                                  __builtin_bit_cast(f16x8_w8_t, b), c, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w8a_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 w8a_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// four bytes b0..b3 (each < 256) as two 16-bit pairs (M + b0, M + b1), (M + b2, M + b3) above the magic byte M
+__device__ __forceinline__ uint32_t w8a_pair_lo(uint32_t magic, uint32_t bytes) {
+  return __builtin_amdgcn_perm(magic, bytes, 0x04010400u);
+}
+__device__ __forceinline__ uint32_t w8a_pair_hi(uint32_t magic, uint32_t bytes) {
+  return __builtin_amdgcn_perm(magic, bytes, 0x04030402u);
+}
+
+constexpr int w8a16_max_threads(int mb, int t) { return mb * t >= 2 ? 512 : 1024; }
+
+template <int MB, int T, bool XBF16, bool SBF16>
+__global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ qw, int64_t ldq,
+    const uint16_t* __restrict__ scales, int64_t lds, const void* __restrict__ bias, int bdt,
+    uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int gsteps, int KS) {
+  constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr float kCorr = XBF16 ? 2304.f : 1152.f;  // 17 * 128 + 128 (bf16 planes) / 1024 + 128 (fp16 bytes)
+  constexpr int NV = T * MB * 4;
+  extern __shared__ __align__(16) float red[];  // [waves][NV][64]
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int BW = (int)(blockDim.x / kWave) / KS;
+  const int ks = wave % KS, nb = blockIdx.x * BW + wave / KS;
+  const int n0 = nb * 16 * T;
+  const int nsteps = K / 128;
+  const int st0 = (int)((int64_t)ks * nsteps / KS), st1 = (int)((int64_t)(ks + 1) * nsteps / KS);
+  const int r16 = lane & 15, j = lane >> 4;
+  const int G = gsteps > 0 ? (nsteps + gsteps - 1) / gsteps : 1;
+
+  const __amdgpu_buffer_rsrc_t rq = w8a_rsrc(qw, (uint32_t)N * (uint32_t)ldq);
+  const __amdgpu_buffer_rsrc_t rx = w8a_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);
+  const __amdgpu_buffer_rsrc_t rs = w8a_rsrc(scales, (uint32_t)G * (uint32_t)lds * 2u);
+  uint32_t woff[T], soff[T];
+  int ncol[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    ncol[t] = min(n0 + 16 * t + r16, N - 1);
+    woff[t] = (uint32_t)ncol[t] * (uint32_t)ldq + 32u * j;
+    soff[t] = (uint32_t)ncol[t];
+  }
+  uint32_t xoff[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) xoff[i] = (uint32_t)min(16 * i + r16, M - 1) * (uint32_t)ldx * 2u + 64u * j;
+  const FastDiv gdiv((uint32_t)max(gsteps, 1));
+  const uint32_t lds32 = (uint32_t)lds;
+
+  struct Buf {
+    uint4 w[T][2], x[MB][4];
+    uint32_t s[T];
+  };
+  Buf bufa, bufb;
+  auto fetch = [&](int st, Buf& b) __attribute__((always_inline)) {
+    const uint32_t g = gsteps > 0 ? gdiv.div((uint32_t)st) : 0u;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b.x[i][q] = w8a_ld16(rx, xoff[i] + (uint32_t)st * 256u + 16u * q);
+#pragma unroll
+    for (int t = 0; t < T; ++t) b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)((g * lds32 + soff[t]) * 2u), 0, 0);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) b.w[t][h] = w8a_ld16(rq, woff[t] + (uint32_t)st * 128u + 16u * h);
+  };
+
+  f32x4_w8_t acc[T][MB];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[t][i] = f32x4_w8_t{0.f, 0.f, 0.f, 0.f};
+  const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
+
+  auto compute = [&](const Buf& b) __attribute__((always_inline)) {
+    f32x4_w8_t xs[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      xs[i] = f32x4_w8_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xs[i] = w8_mfma<XBF16>(b.x[i][s], ones, xs[i]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float sc = SBF16 ? bf16_bits_to_f32(b.s[t]) : f16_bits_to_f32((uint16_t)b.s[t]);
+      const uint32_t wd[8] = {b.w[t][0].x, b.w[t][0].y, b.w[t][0].z, b.w[t][0].w,
+                              b.w[t][1].x, b.w[t][1].y, b.w[t][1].z, b.w[t][1].w};
+      f32x4_w8_t a1[MB], a2[MB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) a1[i] = a2[i] = f32x4_w8_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t u0 = wd[2 * s] ^ 0x80808080u, u1 = wd[2 * s + 1] ^ 0x80808080u;  // q + 128 per byte
+        if constexpr (XBF16) {
+          const uint32_t l0 = u0 & 0x0F0F0F0Fu, l1 = u1 & 0x0F0F0F0Fu;
+          const uint32_t h0 = (u0 >> 4) & 0x0F0F0F0Fu, h1 = (u1 >> 4) & 0x0F0F0F0Fu;
+          const uint4 bl = make_uint4(w8a_pair_lo(0x43434343u, l0), w8a_pair_hi(0x43434343u, l0),
+                                      w8a_pair_lo(0x43434343u, l1), w8a_pair_hi(0x43434343u, l1));
+          const uint4 bh = make_uint4(w8a_pair_lo(0x43434343u, h0), w8a_pair_hi(0x43434343u, h0),
+                                      w8a_pair_lo(0x43434343u, h1), w8a_pair_hi(0x43434343u, h1));
+#pragma unroll
+          for (int i = 0; i < MB; ++i) {
+            a1[i] = w8_mfma<XBF16>(b.x[i][s], bh, a1[i]);
+            a2[i] = w8_mfma<XBF16>(b.x[i][s], bl, a2[i]);
+          }
+        } else {
+          const uint4 bu = make_uint4(w8a_pair_lo(0x64646464u, u0), w8a_pair_hi(0x64646464u, u0),
+                                      w8a_pair_lo(0x64646464u, u1), w8a_pair_hi(0x64646464u, u1));
+#pragma unroll
+          for (int i = 0; i < MB; ++i) a1[i] = w8_mfma<XBF16>(b.x[i][s], bu, a1[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = XBF16 ? __builtin_fmaf(16.f, a1[i][e], a2[i][e]) : a1[i][e];
+          acc[t][i][e] = __builtin_fmaf(sc, __builtin_fmaf(-kCorr, xs[i][e], v), acc[t][i][e]);
+        }
+    }
+  };
+
+  // Steps past the slice re-read its last step (valid, cached) and are not computed.
+  if (st0 < st1) {
+    const int last = st1 - 1;
+    fetch(st0, bufa);
+    fetch(min(st0 + 1, last), bufb);
+    for (int st = st0; st < st1; st += 2) {
+      compute(bufa);
+      fetch(min(st + 2, last), bufa);
+      if (st + 1 < st1) compute(bufb);
+      fetch(min(st + 3, last), bufb);
+    }
+  }
+
+  float* mine = red + (size_t)wave * NV * kWave;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mine[((t * MB + i) * 4 + e) * kWave + lane] = acc[t][i][e];
+  __syncthreads();
+  const float* base = red + (size_t)(wave - ks) * NV * kWave;
+  for (int v = ks; v < NV; v += KS) {
+    float sum = 0.f;
+    for (int k2 = 0; k2 < KS; ++k2) sum += base[((size_t)k2 * NV + v) * kWave + lane];
+    const int t = v / (MB * 4), i = (v / 4) % MB, e = v % 4;
+    const int m = 16 * i + 4 * j + e, n = n0 + 16 * t + r16;
+    if (m < M && n < N) {
+      if (bias) sum += load_f(bias, bdt, n);
+      y[(int64_t)m * ldy + n] = XBF16 ? f32_to_bf16_bits(sum) : f32_to_f16_bits(sum);
+    }
+  }
+}
+
+// Generic: one wavefront per (channel n, up to 4 rows of x); fixed-order lane and cross-lane sums.
+__global__ void __launch_bounds__(256) w8a16_generic_kernel(const void* __restrict__ x, int64_t ldx, int xdt,
+                                                            const int8_t* __restrict__ qw, int64_t ldq,
+                                                            const void* __restrict__ scales, int sdt, int64_t lds,
+                                                            const void* __restrict__ bias, int bdt, void* __restrict__ y,
+                                                            int64_t ldy, int M, int N, int K, int gs) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t item = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int mblocks = (M + 3) / 4;
+  if (item >= (int64_t)N * mblocks) return;  // whole wavefronts leave together
+  const int n = (int)(item / mblocks), m0 = (int)(item % mblocks) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = lane; k < K; k += kWave) {
+    const float w = (float)qw[(int64_t)n * ldq + k] * load_f(scales, sdt, (int64_t)(k / gs) * lds + n);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (m0 + r < M) acc[r] = __builtin_fmaf(load_f(x, xdt, (int64_t)(m0 + r) * ldx + k), w, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = wave_sum(acc[r]);
+    if (lane == 0 && m0 + r < M) store_f(y, xdt, (int64_t)(m0 + r) * ldy + n, bias ? v + load_f(bias, bdt, n) : v);
+  }
+}
+
+bool w8a16_skinny_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int sdt, int64_t lds, int64_t M,
+                     int64_t N, int64_t K, int gs, int64_t G) {
+  const int64_t k4g = 1LL << 32;
+  return M > 0 && M <= 64 && sdt != FG_F32 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) && (ldx % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 &&
+         (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && N * ldq < k4g && M * ldx * 2 < k4g && G * lds * 2 < k4g;
+}
+
+static int w8a_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+// Same shape rules as the W4 skinny kernel (the weight bytes per step double, the register budget is the same):
+// T tiles (4 / 2 / 1, capped by the rows of x) leaving at least 3/4 of a channel block per CU, 2-4 K slices, channel
+// blocks per workgroup chosen so that workgroups spread evenly over the CUs.
+static void w8a16_plan(int M, int N, int K, int* mb, int* T, int* KS, int* BW) {
+  const int cus = w8a_cus();
+  const int b = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  int t = b == 1 ? 4 : (b == 2 ? 2 : 1);
+  while (t > 1 && 4 * ((N + 16 * t - 1) / (16 * t)) < 3 * cus) t /= 2;
+  const int nblk = (N + 16 * t - 1) / (16 * t);
+  const int maxw = w8a16_max_threads(b, t) / kWave;
+  int ks = (b == 1 && t <= 2) ? 4 : 2;
+  ks = max(1, min(ks, K / 128));
+  int best = 1;
+  double best_eff = -1.0;
+  for (int bw = 1; bw <= 4 && bw * ks <= maxw; bw *= 2) {
+    const int wgs = (nblk + bw - 1) / bw;
+    const double eff = ((double)wgs / cus) / ((wgs + cus - 1) / cus);
+    if (eff > best_eff + 1e-9) { best = bw; best_eff = eff; }
+  }
+  *mb = b; *T = t; *KS = ks; *BW = best;
+}
+
+template <int MB, int T, bool XBF16, bool SBF16>
+static hipError_t launch_w8a16_skinny_t(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq,
+                                        const void* scales, int64_t lds, const void* bias, int bdt, void* y,
+                                        int64_t ldy, int M, int N, int K, int gsteps, int KS, int BW, hipStream_t s) {
+  const int nblk = (N + 16 * T - 1) / (16 * T);
+  const size_t shm = (size_t)BW * KS * (T * MB * 4) * kWave * sizeof(float);
+  auto kern = w8a16_skinny_kernel<MB, T, XBF16, SBF16>;
+  if (shm > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3((nblk + BW - 1) / BW), dim3(kWave * BW * KS), shm, s,
+                     static_cast<const uint16_t*>(x), ldx, qw, ldq, static_cast<const uint16_t*>(scales), lds, bias,
+                     bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gsteps, KS);
+  return hipGetLastError();
+}
+
+template <bool XBF16, bool SBF16>
+static hipError_t launch_w8a16_skinny_x(int mb, int T, const void* x, int64_t ldx, const int8_t* qw, int64_t ldq,
+                                        const void* scales, int64_t lds, const void* bias, int bdt, void* y,
+                                        int64_t ldy, int M, int N, int K, int gsteps, int KS, int BW, hipStream_t s) {
+#define FG_W8A(MB_, T_)                                                                                      \
+  return launch_w8a16_skinny_t<MB_, T_, XBF16, SBF16>(x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, \
+                                                      gsteps, KS, BW, s)
+  if (mb == 1) {
+    if (T == 4) FG_W8A(1, 4);
+    if (T == 2) FG_W8A(1, 2);
+    FG_W8A(1, 1);
+  }
+  if (mb == 2) {
+    if (T == 2) FG_W8A(2, 2);
+    FG_W8A(2, 1);
+  }
+  FG_W8A(4, 1);
+#undef FG_W8A
+}
+
+hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                               const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                               int64_t ldy, int M, int N, int K, int gs, bool single_group, hipStream_t s) {
+  int mb, T, KS, BW;
+  w8a16_plan(M, N, K, &mb, &T, &KS, &BW);
+  const int gsteps = single_group ? 0 : gs / 128;
+  const bool sbf = sdt == FG_BF16;
+  if (xbf16) {
+    if (sbf) return launch_w8a16_skinny_x<true, true>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
+    return launch_w8a16_skinny_x<true, false>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
+  }
+  if (sbf) return launch_w8a16_skinny_x<false, true>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
+  return launch_w8a16_skinny_x<false, false>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
+}
+
+hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq,
+                                const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                                int64_t ldy, int M, int N, int K, int gs, hipStream_t s) {
+  const int64_t waves = (int64_t)N * ((M + 3) / 4);
+  hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, ldx, xdt, qw, ldq,
+                     scales, sdt, lds, bias, bdt, y, ldy, M, N, K, gs);
+  return hipGetLastError();
+}
+
+}  // namespace fg

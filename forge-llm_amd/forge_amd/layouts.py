@@ -448,6 +448,115 @@ def quantize_w4_rtn(w: torch.Tensor, group_size: int = 128, sym: bool = True,
     return q.contiguous(), scale.to(scale_dtype), zeros
 
 
+# ------------------------------------------------------------------------------------------------ PackedW8
+@dataclass
+class PackedW8:
+    """Symmetric int8 weight + scales in the portable_row W8 layout (``w8.py:18-80``): ``qweight int8 [N, K]``,
+    ``scales [G, N]`` (column-contiguous per group), per-channel (``group_size <= 0``) or grouped along K."""
+
+    qweight: torch.Tensor
+    scales: torch.Tensor
+    layout: Layout
+    n: int
+    k: int
+    group_size: int
+    meta: dict[str, Any] = field(default_factory=dict)
+
+    @property
+    def layout_id(self) -> str:
+        return self.layout.id
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.n, self.k)
+
+    @property
+    def num_groups(self) -> int:
+        return int(self.scales.shape[0])
+
+    @property
+    def device(self) -> torch.device:
+        return self.qweight.device
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.qweight, self.scales))
+
+    @property
+    def bits_per_weight(self) -> float:
+        return 8.0 * self.nbytes / max(1, self.n * self.k)
+
+    def to(self, device: Any = None, dtype: torch.dtype | None = None) -> PackedW8:
+        return PackedW8(self.qweight.to(device or self.qweight.device),
+                        self.scales.to(device=device or self.scales.device, dtype=dtype or self.scales.dtype),
+                        self.layout, self.n, self.k, self.group_size, dict(self.meta))
+
+    def unpack(self) -> tuple[torch.Tensor, torch.Tensor]:
+        return unpack_w8(self)
+
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """Dense ``[N, K]`` weight ``q * s`` in fp32 (exact), cast to ``dtype`` (``w8.py:54-56,101-104``)."""
+        q, s = unpack_w8(self)
+        return dequantize_w8_parts(q, s, self.group_size).to(dtype)
+
+    def tensors(self) -> dict[str, torch.Tensor]:
+        return {"qweight": self.qweight, "scales": self.scales}
+
+    @staticmethod
+    def tensor_roles() -> dict[str, str]:
+        return {"qweight": "payload", "scales": "scale"}
+
+    def state(self) -> dict[str, Any]:
+        return {"layout_id": self.layout.id, "layout": self.layout.to_dict(), "n": self.n, "k": self.k,
+                "group_size": self.group_size, "scale_dtype": str(self.scales.dtype).replace("torch.", "")}
+
+    @classmethod
+    def from_tensors(cls, tensors: dict[str, torch.Tensor], state: dict[str, Any]) -> PackedW8:
+        lay = get_layout(state["layout_id"]) if state.get("layout_id") in _REG else Layout.from_dict(state["layout"])
+        return cls(tensors["qweight"], tensors["scales"], lay, int(state["n"]), int(state["k"]), int(state["group_size"]))
+
+
+def pack_w8(q: torch.Tensor, scales: torch.Tensor, group_size: int = -1, layout: Layout | str | None = None) -> PackedW8:
+    """``q int8 [N, K]``, ``scales [N, G]`` -> :class:`PackedW8` (``w8.py:83-94``: scales stored transposed)."""
+    lay = PORTABLE_W8 if layout is None else (get_layout(layout) if isinstance(layout, str) else layout)
+    if lay.bits != 8:
+        raise ConfigError(f"layout {lay.id} is not an 8-bit layout")
+    if q.dim() != 2 or q.dtype != torch.int8:
+        raise ConfigError("q must be int8 [N, K]")
+    n, k = q.shape
+    g = num_groups(k, group_size)
+    if tuple(scales.shape) != (n, g):
+        raise ConfigError(f"scales must be [N={n}, G={g}], got {tuple(scales.shape)}")
+    return PackedW8(q.contiguous(), scales.t().contiguous(), lay, n, k, int(group_size))
+
+
+def unpack_w8(p: PackedW8) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(q int8 [N, K], scales [N, G])`` (``w8.py:97-98``)."""
+    return p.qweight, p.scales.t().contiguous()
+
+
+def dequantize_w8_parts(q: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    """``W[n, k] = q[n, k] * scales[n, k // gs]`` in fp32 (``w8.py:101-104``); exact, as int8 x fp16 fits fp32."""
+    n, k = q.shape
+    gi = torch.arange(k, device=q.device) // effective_group(group_size, k)
+    return q.float() * scales.float()[:, gi]
+
+
+def quantize_w8_rtn(w: torch.Tensor, group_size: int = -1,
+                    scale_dtype: torch.dtype = torch.float16) -> tuple[torch.Tensor, torch.Tensor]:
+    """Round-to-nearest symmetric int8 (``rtn.py:60-72``): ``scale = amax / 127`` rounded to ``scale_dtype``,
+    ``q = clamp(round(w / scale), -128, 127)``; returns ``(q int8 [N, K], scales [N, G])``."""
+    if w.dim() != 2:
+        raise ConfigError("w must be [N, K]")
+    n, k = w.shape
+    wg, g, gs = _grouped(w, group_size)
+    wz = torch.where(torch.isnan(wg), torch.zeros_like(wg), wg)
+    scale = (wz.abs().amax(dim=-1) / 127.0).clamp_min(1e-12)
+    scale = scale.to(scale_dtype).float().clamp_min(1e-12)
+    q = torch.round(wz / scale.unsqueeze(-1)).clamp(-128, 127)
+    return q.reshape(n, g * gs)[:, :k].to(torch.int8).contiguous(), scale.to(scale_dtype)
+
+
 def require_portable(p: PackedW4) -> None:
     if p.layout.kind != KIND_PORTABLE:
         raise ConfigError(f"the gfx950 W4A16 kernels need the portable_row layout, got {p.layout_id}; repack() first")
@@ -456,7 +565,8 @@ def require_portable(p: PackedW4) -> None:
 __all__ = [
     "FRAGMENT_W4", "GROUP_SORT_KEY", "HardwareUnsupported", "IDENTITY_INTERLEAVE", "KIND_FRAGMENT", "KIND_PORTABLE",
     "KIND_PORTABLE_ROW", "Layout", "MARLIN_INTERLEAVE", "MISSING_SORT", "PORTABLE_W4", "PORTABLE_W8", "PackedW4",
-    "cached_group_sort", "ceil_div", "effective_group", "fragment_layout", "fragment_tile_perm", "get_layout",
-    "known_layouts", "num_groups", "pack_nibbles_int32", "pack_w4", "portable_layout", "quantize_w4_rtn",
-    "register_layout", "repack", "roundup", "sort_columns_by_group", "unpack_nibbles_int32", "unpack_w4",
+    "PackedW8", "cached_group_sort", "ceil_div", "dequantize_w8_parts", "effective_group", "fragment_layout",
+    "fragment_tile_perm", "get_layout", "known_layouts", "num_groups", "pack_nibbles_int32", "pack_w4", "pack_w8",
+    "portable_layout", "quantize_w4_rtn", "quantize_w8_rtn", "register_layout", "repack", "roundup",
+    "sort_columns_by_group", "unpack_nibbles_int32", "unpack_w4", "unpack_w8",
 ]

@@ -29,13 +29,18 @@ from .layouts import (
     KIND_PORTABLE,
     MISSING_SORT,
     PORTABLE_W4,
+    PORTABLE_W8,
     Layout,
     PackedW4,
+    PackedW8,
     cached_group_sort,
     effective_group,
     get_layout,
+    num_groups,
     pack_w4,
+    pack_w8,
     quantize_w4_rtn,
+    quantize_w8_rtn,
     repack,
     roundup,
 )
@@ -107,6 +112,12 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
     return x2
 
 
+def _ld(t: torch.Tensor) -> int:
+    """Row stride for the C ABI: the dim-0 stride, or the row length for a one-row tensor (torch counts a one-row
+    tensor contiguous whatever its dim-0 stride is, so that stride can be smaller than a row)."""
+    return int(t.stride(0)) if t.shape[0] > 1 else int(t.shape[1])
+
+
 # ------------------------------------------------------------------------------------------------ W4A16
 def _data_stamp(*ts: torch.Tensor | None) -> tuple:
     return tuple((t.data_ptr(), t._version, tuple(t.shape), str(t.device)) for t in ts if t is not None)
@@ -163,16 +174,16 @@ def _w4_launch(x2: torch.Tensor, p: PackedW4, perm: torch.Tensor | None, g_idx: 
     m, k = x2.shape
     n = p.n
     gs = p.group_size
-    x_aligned = int(x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0)
-    q_aligned = int(p.qweight.stride(0) % 4 == 0 and p.qweight.data_ptr() % 16 == 0)
+    x_aligned = int(_ld(x2) % 8 == 0 and x2.data_ptr() % 16 == 0)
+    q_aligned = int(_ld(p.qweight) % 4 == 0 and p.qweight.data_ptr() % 16 == 0)
     cfgp = None if cfg is None else _lib.ctypes.byref(cfg)
     ws_bytes = L.fg_w4a16_workspace_bytes(m, n, k, gs, x_aligned, q_aligned, int(g_idx is not None), cfgp)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
     zeros = p.zeros
     _lib.check(L.fg_w4a16_gemm(
-        _lib.ptr(x2), x2.stride(0), _lib.dtype_code(x2.dtype), _lib.ptr(p.qweight), p.qweight.stride(0),
-        _lib.ptr(p.scales), _lib.dtype_code(p.scales.dtype), p.scales.stride(0),
-        _lib.ptr(zeros), 0 if zeros is None else zeros.stride(0), _lib.ptr(perm), _lib.ptr(g_idx),
+        _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(p.qweight), _ld(p.qweight),
+        _lib.ptr(p.scales), _lib.dtype_code(p.scales.dtype), _ld(p.scales),
+        _lib.ptr(zeros), 0 if zeros is None else _ld(zeros), _lib.ptr(perm), _lib.ptr(g_idx),
         _lib.ptr(bias), _lib.dtype_code(bias.dtype) if bias is not None else 0,
         _lib.ptr(y), y.stride(0), m, n, k, gs, p.num_groups, cfgp, _lib.ptr(ws), ws_bytes, _lib.stream_of(x2)),
         "fg_w4a16_gemm")
@@ -220,6 +231,50 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     return y.reshape(*lead, p.n)
 
 
+# ------------------------------------------------------------------------------------------------ W8A16
+def w8a16_linear(x: torch.Tensor, packed: PackedW8, bias: torch.Tensor | None = None, *,
+                 config: dict[str, Any] | None = None, deterministic: bool = True) -> torch.Tensor:
+    """``y = x @ dequant(Wq)^T + bias`` with symmetric int8 weights (``forge/kernels/ops_gemm.py:320-346``) for
+    ``x [..., K]`` bf16/fp16 on a gfx950 GPU (returns ``x.dtype``).
+
+    ``fg_w8a16_gemm`` picks the skinny MFMA kernel for M <= 64, the dequantise-to-LDS MFMA kernel beyond, and a
+    generic kernel for shapes neither takes (override with ``config={"impl": "mfma"|"prefill"|"generic"}``).  Every
+    path reduces in a fixed order, so results are run-to-run reproducible.
+    """
+    _ready(x, "w8a16_linear")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise HardwareUnsupported(f"w8a16_linear: activations must be bf16 or fp16, got {x.dtype}")
+    if x.shape[-1] != packed.k:
+        raise ConfigError(f"x has K={x.shape[-1]} but the packed weight has K={packed.k}")
+    if packed.layout.bits != 8:
+        raise ConfigError(f"layout {packed.layout_id} is not an 8-bit layout")
+    if packed.qweight.device != x.device:
+        raise ConfigError(f"weight on {packed.qweight.device} but x on {x.device}")
+    lead = x.shape[:-1]
+    x2 = _rows(x)
+    m = x2.shape[0]
+    y = torch.empty((m, packed.n), dtype=x.dtype, device=x.device)
+    if m == 0:
+        _note("w8a16_linear")
+        return y.reshape(*lead, packed.n)
+    q = packed.qweight if packed.qweight.stride(-1) == 1 else packed.qweight.contiguous()
+    sc = packed.scales if packed.scales.stride(-1) == 1 else packed.scales.contiguous()
+    b = None if bias is None else bias.contiguous()
+    cfg = _w4_config(config)
+    cfgp = None if cfg is None else _lib.ctypes.byref(cfg)
+    L = _lib.lib()
+    ws_bytes = L.fg_w8a16_workspace_bytes(m, packed.n, packed.k, packed.group_size, cfgp)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.check(L.fg_w8a16_gemm(
+        _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(q), _ld(q), _lib.ptr(sc),
+        _lib.dtype_code(sc.dtype), _ld(sc), _lib.ptr(b),
+        _lib.dtype_code(b.dtype) if b is not None else 0,
+        _lib.ptr(y), y.stride(0), m, packed.n, packed.k, packed.group_size, packed.num_groups, cfgp, _lib.ptr(ws),
+        ws_bytes, _lib.stream_of(x2)), "fg_w8a16_gemm")
+    _note("w8a16_linear")
+    return y.reshape(*lead, packed.n)
+
+
 def w4_dequant(packed: PackedW4, dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Dense ``[N, K]`` dequantisation on the GPU (``fg_w4_dequant``): ``(q - z) * s`` in fp32, one rounding."""
     p = _portable(packed)
@@ -229,9 +284,9 @@ def w4_dequant(packed: PackedW4, dtype: torch.dtype = torch.float32) -> torch.Te
     out = torch.empty((p.n, p.k), dtype=dtype, device=p.qweight.device)
     z = p.zeros
     L = _lib.lib()
-    _lib.check(L.fg_w4_dequant(_lib.ptr(p.qweight), p.qweight.stride(0), _lib.ptr(p.scales),
-                               _lib.dtype_code(p.scales.dtype), p.scales.stride(0), _lib.ptr(z),
-                               0 if z is None else z.stride(0), _lib.ptr(p.g_idx), _lib.ptr(out), _lib.dtype_code(dtype),
+    _lib.check(L.fg_w4_dequant(_lib.ptr(p.qweight), _ld(p.qweight), _lib.ptr(p.scales),
+                               _lib.dtype_code(p.scales.dtype), _ld(p.scales), _lib.ptr(z),
+                               0 if z is None else _ld(z), _lib.ptr(p.g_idx), _lib.ptr(out), _lib.dtype_code(dtype),
                                out.stride(0), p.n, p.k, p.group_size, p.num_groups, _lib.stream_of(out)),
                "fg_w4_dequant")
     _note("w4_dequant")
@@ -259,7 +314,7 @@ def _quant_fp8_block(x2: torch.Tensor, bm: int, bk: int, scale: torch.Tensor | N
         static, out_s = None, s
     if m:
         _lib.check(_lib.lib().fg_quant_fp8_block(
-            _lib.ptr(x2), x2.stride(0), _lib.dtype_code(x2.dtype), _lib.ptr(q), q.stride(0), _lib.ptr(out_s),
+            _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(q), _ld(q), _lib.ptr(out_s),
             kb, m, k, bm, bk, _lib.ptr(static), _lib.stream_of(x2)), "fg_quant_fp8_block")
     return q, s
 
@@ -300,7 +355,7 @@ def quantize_act_fp8(x: torch.Tensor, *, granularity: str = "per_token", block: 
         w = None if rms_weight is None else rms_weight.contiguous()
         if m:
             _lib.check(L.fg_quant_fp8_rowwise(
-                _lib.ptr(x2), x2.stride(0), _lib.dtype_code(x2.dtype), _lib.ptr(q), q.stride(0),
+                _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(q), _ld(q),
                 _lib.ptr(None if st is not None else s), m, k, _lib.ptr(st), _lib.ptr(w),
                 _lib.dtype_code(w.dtype) if w is not None else 0, float(rms_eps or 0.0), int(rms_eps is not None),
                 _lib.stream_of(x2)), "fg_quant_fp8_rowwise")
@@ -406,7 +461,7 @@ def fp8_linear(x: torch.Tensor, w_fp8: torch.Tensor, w_scale: torch.Tensor, bias
     b = None if bias is None else bias.contiguous()
     cfg = _mm_config(config)
     _lib.check(_lib.lib().fg_fp8_gemm(
-        _lib.ptr(a), a.stride(0), _lib.ptr(sa), sam, sak, _lib.ptr(wq), wq.stride(0), _lib.ptr(sb), sbn, sbk, sb_div,
+        _lib.ptr(a), _ld(a), _lib.ptr(sa), sam, sak, _lib.ptr(wq), _ld(wq), _lib.ptr(sb), sbn, sbk, sb_div,
         mode, block, _lib.ptr(b), _lib.dtype_code(b.dtype) if b is not None else 0, _lib.ptr(y), y.stride(0),
         _lib.dtype_code(odt), m, n, k, None if cfg is None else _lib.ctypes.byref(cfg), _lib.stream_of(a)),
         "fg_fp8_gemm")
@@ -427,8 +482,8 @@ def quantize_act_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     q = torch.empty((m, k), dtype=torch.int8, device=x.device)
     s = torch.empty(m, dtype=torch.float32, device=x.device)
     if m:
-        _lib.check(_lib.lib().fg_quant_int8_rowwise(_lib.ptr(x2), x2.stride(0), _lib.dtype_code(x2.dtype), _lib.ptr(q),
-                                                    q.stride(0), _lib.ptr(s), m, k, _lib.stream_of(x2)),
+        _lib.check(_lib.lib().fg_quant_int8_rowwise(_lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(q),
+                                                    _ld(q), _lib.ptr(s), m, k, _lib.stream_of(x2)),
                    "fg_quant_int8_rowwise")
     _note("quantize_act_int8")
     return q.reshape(shape), s
@@ -461,7 +516,7 @@ def int8_gemm(xq: torch.Tensor, sx: torch.Tensor | None, wq: torch.Tensor, sw: t
     b = None if bias is None else bias.contiguous()
     cfg = _mm_config(config)
     _lib.check(_lib.lib().fg_int8_gemm(
-        _lib.ptr(a), a.stride(0), _lib.ptr(sa), sal, _lib.ptr(w), w.stride(0), _lib.ptr(sb), sbl, _lib.ptr(b),
+        _lib.ptr(a), _ld(a), _lib.ptr(sa), sal, _lib.ptr(w), _ld(w), _lib.ptr(sb), sbl, _lib.ptr(b),
         _lib.dtype_code(b.dtype) if b is not None else 0, _lib.ptr(y), y.stride(0), _lib.dtype_code(out_dtype),
         m, n, k, None if cfg is None else _lib.ctypes.byref(cfg), _lib.stream_of(a)), "fg_int8_gemm")
     return y.reshape(*lead, n)
@@ -680,10 +735,60 @@ class KernelInt8Linear(_KernelLinear):
         return int8_linear(x, self.weight_int8, self.weight_scale, self._bias(x))
 
 
-PACKED_LINEAR_CLASSES: dict[str, type] = {"w4a16": KernelW4A16Linear, "fp8": KernelFp8Linear, "int8": KernelInt8Linear}
+class KernelW8A16Linear(_KernelLinear):
+    """8-bit weight-only linear backed by :func:`w8a16_linear` (``forge/kernels/ops_gemm.py:843-887``; buffers
+    ``qweight int8 [N, K]`` and ``scales [G, N]``)."""
+
+    kind: ClassVar[str] = "w8a16"
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False, dtype: torch.dtype | None = None,
+                 device: Any = None, *, group_size: int = -1, **_: Any):
+        super().__init__(in_features, out_features, bias, dtype, device)
+        self.group_size = int(group_size)
+        g = num_groups(in_features, group_size)
+        self.register_buffer("qweight", torch.zeros((out_features, in_features), dtype=torch.int8, device=device))
+        self.register_buffer("scales", torch.zeros((g, out_features), dtype=dtype or torch.float16, device=device))
+
+    @classmethod
+    def from_packed(cls, packed: PackedW8, bias: torch.Tensor | None = None) -> KernelW8A16Linear:
+        m = cls(packed.k, packed.n, bias is not None, packed.scales.dtype, packed.qweight.device,
+                group_size=packed.group_size)
+        with torch.no_grad():
+            m.qweight.copy_(packed.qweight)
+            m.scales.copy_(packed.scales)
+            if bias is not None:
+                m.bias.data = bias.detach().clone()
+        return m
+
+    @classmethod
+    def from_dense(cls, linear: nn.Linear, *, group_size: int = -1, scale_dtype: torch.dtype = torch.float16,
+                   **_: Any) -> KernelW8A16Linear:
+        q, s = quantize_w8_rtn(linear.weight.detach(), group_size, scale_dtype)
+        return cls.from_packed(pack_w8(q, s, group_size), linear.bias.detach() if linear.bias is not None else None)
+
+    @classmethod
+    def from_shape(cls, in_features: int, out_features: int, bias: bool = False, dtype: torch.dtype | None = None,
+                   device: Any = None, **kw: Any):
+        return cls(in_features, out_features, bias, dtype, device, **kw)
+
+    def packed(self) -> PackedW8:
+        return PackedW8(self.qweight, self.scales, PORTABLE_W8, self.out_features, self.in_features, self.group_size)
+
+    def dequantize(self, dtype: torch.dtype | None = None) -> torch.Tensor:
+        return self.packed().dequantize(dtype or torch.float32)
+
+    def quant_spec(self) -> dict[str, Any]:
+        return {"bits": 8, "group_size": self.group_size, "layout": PORTABLE_W8.id}
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return w8a16_linear(x, self.packed(), self._bias(x))
 
 
-def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: PackedW4 | None = None,
+PACKED_LINEAR_CLASSES: dict[str, type] = {"w4a16": KernelW4A16Linear, "w8a16": KernelW8A16Linear,
+                                          "fp8": KernelFp8Linear, "int8": KernelInt8Linear}
+
+
+def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: PackedW4 | PackedW8 | None = None,
                        bias: torch.Tensor | None = None, in_features: int | None = None,
                        out_features: int | None = None, **kw: Any) -> nn.Module:
     """Factory of kernel-backed packed linears (``forge/kernels/ops_gemm.py:1025-1068``, GEMM-family kinds)."""
@@ -692,6 +797,8 @@ def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: Pa
         raise ConfigError(f"unknown packed linear kind {kind!r}; choose from {sorted(PACKED_LINEAR_CLASSES)}")
     if packed is not None:
         if isinstance(packed, PackedW4) and cls is KernelW4A16Linear:
+            return cls.from_packed(packed, bias)
+        if isinstance(packed, PackedW8) and cls is KernelW8A16Linear:
             return cls.from_packed(packed, bias)
         raise ConfigError(f"packed data of type {type(packed).__name__} does not match kind {kind!r}")
     if linear is not None:
@@ -702,8 +809,8 @@ def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: Pa
 
 
 __all__ = [
-    "KernelFp8Linear", "KernelInt8Linear", "KernelW4A16Linear", "PACKED_LINEAR_CLASSES", "force_ref", "forced_impl",
-    "fp8_linear", "int8_gemm", "int8_linear", "kernel_debug", "kernel_strict", "last_path", "make_packed_linear",
-    "prepare_fp8_scales", "prepare_w4", "quantize_act_fp8", "quantize_act_int8", "quantize_weight_fp8",
-    "reset_failure_memo", "w4_dequant", "w4a16_linear",
+    "KernelFp8Linear", "KernelInt8Linear", "KernelW4A16Linear", "KernelW8A16Linear", "PACKED_LINEAR_CLASSES",
+    "force_ref", "forced_impl", "fp8_linear", "int8_gemm", "int8_linear", "kernel_debug", "kernel_strict",
+    "last_path", "make_packed_linear", "prepare_fp8_scales", "prepare_w4", "quantize_act_fp8", "quantize_act_int8",
+    "quantize_weight_fp8", "reset_failure_memo", "w4_dequant", "w4a16_linear", "w8a16_linear",
 ]

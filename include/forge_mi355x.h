@@ -102,6 +102,23 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
                   int64_t N, int64_t K, int32_t group_size, int32_t n_groups, fg_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * W8A16:  y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+ bias),  W[n,k] = q[n,k] * scale[g(k), n],  q signed int8 (symmetric).
+ * Replaces the Triton launcher behind w8a16_linear: forge/kernels/ops_gemm.py:320-346 ->
+ * forge/kernels/triton/gemm_w8a16.py:14-31 (wq_gemm with bits=8, forge/kernels/triton/gemm_wq.py:138-205).
+ *   x        bf16|fp16 [M, K] (row stride ldx)
+ *   qweight  int8 [N, K] (row stride ldq, bytes; portable_row PackedW8, forge/kernels/layouts/w8.py:18-104)
+ *   scales   fp16|bf16|fp32 [G, N] (row stride lds);  group_size <= 0: one group per row (per-channel)
+ *   cfg      NULL (policy) or impl FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL (dequantise-to-LDS kernel),
+ *            FG_W4_GENERIC (any shape); split_k for the prefill kernel
+ *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernel; 0 otherwise)
+ * ------------------------------------------------------------------------------------------------------------- */
+size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, const fg_w4_config* cfg);
+int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
+                  int scale_dtype, int64_t lds, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M,
+                  int64_t N, int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg,
+                  void* workspace, size_t workspace_bytes, fg_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * INT8 W8A8:  acc[M,N] = a[M,K] @ b[N,K]^T in exact int32;  y = (float(acc) * sa[m]) * sb[n] (+ bias[n]).
  * Replaces forge/kernels/triton/gemm_int8.py:95-137 (int8_gemm_triton), called from int8_linear
  * (forge/kernels/ops_gemm.py:483-515).

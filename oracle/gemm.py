@@ -2,6 +2,7 @@
 
 Reference files:
 * ``forge/kernels/ref/gemm_w4a16.py:9-27``  -- W4A16: dequantise to fp32, ``x.float() @ W.T (+ bias.float())``
+* ``forge/kernels/ref/gemm_w4a16.py:45-52`` -- W8A16: ``q * s`` in fp32, then the same GEMM
 * ``forge/kernels/ref/gemm_fp8.py:22-127`` -- FP8 e4m3fn quantiser (per-tensor / per-token / 1xB / BxB), dequant, GEMM
 * ``forge/kernels/ref/gemm_int8.py:8-85``  -- INT8 per-token/channel quantiser, exact int32 GEMM, fp32 epilogue
 * ``forge/kernels/ref/gemm_common.py:27-80`` -- ``compare`` tolerance rule
@@ -85,6 +86,37 @@ def w4a16_gemm_ref(x: np.ndarray, packed: dict, bias: np.ndarray | None = None) 
     q, s, z = unpack_w4(packed)
     w = dequantize_parts(q, s.astype(np.float32), z, packed["group_size"], packed["g_idx"])
     y = np.asarray(x, dtype=np.float32) @ w.T
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float32)
+    return y.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------------- W8A16
+def pack_w8(q: np.ndarray, scales: np.ndarray, group_size: int = -1) -> dict:
+    """Portable_row W8 (``forge/kernels/layouts/w8.py:83-94``): ``qweight int8 [N, K]`` as given, ``scales [N, G]``
+    stored transposed as ``[G, N]``."""
+    q = np.asarray(q, dtype=np.int8)
+    n, k = q.shape
+    gs = k if group_size is None or group_size <= 0 else int(group_size)
+    g = -(-k // gs)
+    s = np.asarray(scales)
+    if s.shape != (n, g):
+        raise ValueError(f"scales must be [N={n}, G={g}], got {s.shape}")
+    return {"qweight": q.copy(), "scales": np.ascontiguousarray(s.T), "n": n, "k": k, "group_size": int(group_size)}
+
+
+def dequantize_w8(packed: dict) -> np.ndarray:
+    """``W[n, k] = q[n, k] * scales[k // gs, n]`` in float32 (``forge/kernels/layouts/w8.py:101-104``)."""
+    q, s = packed["qweight"], np.asarray(packed["scales"], dtype=np.float32)
+    n, k = q.shape
+    gs = k if packed["group_size"] <= 0 else packed["group_size"]
+    gi = np.arange(k) // gs
+    return (q.astype(np.float32) * s[gi, :].T).astype(np.float32)
+
+
+def w8a16_gemm_ref(x: np.ndarray, packed: dict, bias: np.ndarray | None = None) -> np.ndarray:
+    """``Y = X @ dequant(Wq)^T + bias`` in fp32 (``forge/kernels/ref/gemm_w4a16.py:45-52``)."""
+    y = np.asarray(x, dtype=np.float32) @ dequantize_w8(packed).T
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float32)
     return y.astype(np.float32)

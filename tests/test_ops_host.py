@@ -98,3 +98,33 @@ def test_packed_linear_modules_keep_reference_buffer_names():
     fresh = ops.make_packed_linear("w4a16", in_features=96, out_features=40, bias=lin.bias, group_size=32)
     fresh.load_state_dict(w4.state_dict())
     assert torch.equal(fresh.qweight, w4.qweight) and torch.equal(fresh.scales, w4.scales)
+
+
+def test_w8_packer_matches_oracle_and_module_surface():
+    """PackedW8 (forge/kernels/layouts/w8.py:18-104): same bytes as the oracle packer, exact dequantisation, the
+    reference's RTN (scale = amax / 127 rounded to fp16, q clamped to [-128, 127]) and the module's buffer names."""
+    import numpy as np
+
+    from oracle import gemm as og
+
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(40, 96, generator=g)
+    q, s = L.quantize_w8_rtn(w, 32)
+    assert q.dtype == torch.int8 and s.dtype == torch.float16 and s.shape == (40, 3)
+    amax = w.view(40, 3, 32).abs().amax(-1)
+    assert torch.equal(s, (amax / 127.0).clamp_min(1e-12).to(torch.float16))
+    assert (w.view(40, 3, 32) / s.float().unsqueeze(-1) - q.view(40, 3, 32).float()).abs().max() <= 0.5 + 1e-4
+    p = L.pack_w8(q, s, 32)
+    op = og.pack_w8(q.numpy(), s.float().numpy(), 32)
+    assert np.array_equal(p.qweight.numpy(), op["qweight"]) and np.array_equal(p.scales.float().numpy(), op["scales"])
+    assert np.array_equal(p.dequantize().numpy(), og.dequantize_w8(op))
+    assert p.layout_id == "w8.portable_row.v1-db2653" and p.num_groups == 3
+    q2, s2 = L.unpack_w8(p)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    m = ops.make_packed_linear("w8a16", packed=p, bias=torch.zeros(40))
+    assert set(m.state_dict()) == {"bias", "qweight", "scales"} and m.scales.shape == (3, 40)
+    assert m.quant_spec() == {"bits": 8, "group_size": 32, "layout": "w8.portable_row.v1-db2653"}
+    with pytest.raises(ConfigError):
+        L.pack_w8(q, s[:, :2], 32)
+    with pytest.raises(ConfigError):
+        ops.make_packed_linear("w4a16", packed=p)

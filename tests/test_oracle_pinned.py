@@ -117,6 +117,29 @@ def test_w4a16_ref_equals_float64_dequant_then_matmul(m, n, k, gs):
     np.testing.assert_allclose(y, expect, rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("m", [0, 1, 5, 33])
+@pytest.mark.parametrize("n,k,gs", [(7, 100, 32), (64, 65, -1), (130, 256, 128)])
+def test_w8a16_ref_equals_float64_brute_force(m, n, k, gs):
+    """W8A16 oracle (forge/kernels/ref/gemm_w4a16.py:45-52): element-by-element q * s (exact in fp32: an int8 times an
+    fp16-representable scale has at most 19 significant bits) against float64, and the packed scale transpose."""
+    rng = np.random.default_rng(n * k)
+    g = -(-k // (k if gs <= 0 else gs))
+    q = rng.integers(-128, 128, size=(n, k), dtype=np.int64).astype(np.int8)
+    s = (rng.random((n, g)) * 0.02 + 0.001).astype(np.float16).astype(np.float32)
+    p = og.pack_w8(q, s, gs)
+    assert p["scales"].shape == (g, n) and np.array_equal(p["scales"], s.T) and np.array_equal(p["qweight"], q)
+    gsz = k if gs <= 0 else gs
+    w = og.dequantize_w8(p)
+    for (r, c) in [(0, 0), (n - 1, k - 1), (n // 2, k // 3), (1, gsz - 1 if gsz < k else k - 1)]:
+        assert w[r, c] == np.float32(np.float64(q[r, c]) * np.float64(s[r, c // gsz]))
+    x = rnd(m, k, seed=5)
+    bias = rnd(n, seed=6)
+    y = og.w8a16_gemm_ref(x, p, bias)
+    expect = x.astype(np.float64) @ (q.astype(np.float64) * s[:, np.arange(k) // gsz]).T + bias
+    assert y.shape == (m, n) and y.dtype == np.float32
+    np.testing.assert_allclose(y, expect, rtol=1e-5, atol=1e-4)
+
+
 def test_w4a16_ref_g_idx_act_order_and_column_sort():
     rng = np.random.default_rng(5)
     n, k, gs = 16, 64, 16
