@@ -448,6 +448,56 @@ def quantize_w4_rtn(w: torch.Tensor, group_size: int = 128, sym: bool = True,
     return q.contiguous(), scale.to(scale_dtype), zeros
 
 
+# ------------------------------------------------------------------------------------------------ simple int4
+SIMPLE_LAYOUT_ID = "forge.simple.v1"
+
+
+def pack_simple_int4(codes: torch.Tensor) -> torch.Tensor:
+    """Codes ``[N, K]`` (values < 16) in the compress pipeline's "simple" layout (``forge/formats/packing.py:1-5``):
+    ``uint8 [N, ceil(K/2)]``, element ``k`` in byte ``k // 2`` at bit offset ``4 * (k % 2)`` (even = low nibble)."""
+    c = codes.to(torch.uint8)
+    n, k = c.shape
+    if k % 2:
+        c = torch.nn.functional.pad(c, (0, 1))
+    return (c[:, 0::2] | (c[:, 1::2] << 4)).contiguous()
+
+
+def unpack_simple_int4(q8: torch.Tensor, k: int) -> torch.Tensor:
+    """Inverse of :func:`pack_simple_int4`: ``uint8 [N, ceil(K/2)]`` -> codes ``uint8 [N, K]``."""
+    lo, hi = q8 & 0xF, q8 >> 4
+    return torch.stack((lo, hi), dim=-1).reshape(q8.shape[0], -1)[:, :k].contiguous()
+
+
+def pack_w4_from_simple(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor | None, group_size: int,
+                        k: int) -> PackedW4:
+    """A ``forge.simple.v1`` int4 weight (``forge/compress/packed.py:9-12,265-274``: ``qweight uint8 [N, K/2]``,
+    ``scales [N, G]``, ``zeros uint8 [N, G]`` or None) as a portable_row :class:`PackedW4`, bit-identical to
+    ``pack_w4(codes, scales, zeros, group_size)``.  Both formats put code ``k`` at bit ``4 * (k % 8)`` of the
+    little-endian 32-bit word ``k // 8``, so for ``K % 8 == 0`` the packed weights are the same bytes and are reused
+    as an int32 view (no copy); scales are transposed and zero-points packed eight channels per word."""
+    if qweight.dtype != torch.uint8 or qweight.dim() != 2 or qweight.shape[1] != (k + 1) // 2:
+        raise ConfigError(f"simple int4 qweight must be uint8 [N, ceil(K/2)={(k + 1) // 2}], got "
+                          f"{tuple(qweight.shape)} {qweight.dtype}")
+    if k % 8 != 0:  # the portable layout pads K to 8 with the zero-point code: go through the codes
+        return pack_w4(unpack_simple_int4(qweight, k), scales, zeros, group_size)
+    n = qweight.shape[0]
+    if group_size is not None and group_size > 0 and group_size % 8 != 0:
+        raise ConfigError(f"group_size must be -1 or a multiple of 8, got {group_size}")
+    g = num_groups(k, group_size)
+    if tuple(scales.shape) != (n, g) or (zeros is not None and tuple(zeros.shape) != (n, g)):
+        raise ConfigError(f"scales / zeros must be [N={n}, G={g}]")
+    if zeros is not None and int(zeros.to(torch.int16).max()) > 15:
+        raise ConfigError("zeros must be in 0..15")
+    qw = qweight.contiguous().view(torch.int32)
+    zq = None
+    if zeros is not None:  # channels past N in the last word are 0, as pack_w4 writes them
+        zt = torch.zeros((g, roundup(n, 8)), dtype=torch.uint8, device=qweight.device)
+        zt[:, :n] = zeros.to(torch.uint8).t()
+        zq = pack_nibbles_int32(zt.view(g, -1, 8))
+    return PackedW4(qw, scales.t().contiguous(), zq, PORTABLE_W4, n, k, int(group_size), None,
+                    {"n_pad": n, "k_pad": k})
+
+
 # ------------------------------------------------------------------------------------------------ PackedW8
 @dataclass
 class PackedW8:
@@ -565,8 +615,8 @@ def require_portable(p: PackedW4) -> None:
 __all__ = [
     "FRAGMENT_W4", "GROUP_SORT_KEY", "HardwareUnsupported", "IDENTITY_INTERLEAVE", "KIND_FRAGMENT", "KIND_PORTABLE",
     "KIND_PORTABLE_ROW", "Layout", "MARLIN_INTERLEAVE", "MISSING_SORT", "PORTABLE_W4", "PORTABLE_W8", "PackedW4",
-    "PackedW8", "cached_group_sort", "ceil_div", "dequantize_w8_parts", "effective_group", "fragment_layout",
-    "fragment_tile_perm", "get_layout", "known_layouts", "num_groups", "pack_nibbles_int32", "pack_w4", "pack_w8",
+    "PackedW8", "SIMPLE_LAYOUT_ID", "cached_group_sort", "ceil_div", "dequantize_w8_parts", "effective_group", "fragment_layout",
+    "fragment_tile_perm", "get_layout", "known_layouts", "num_groups", "pack_nibbles_int32", "pack_simple_int4", "pack_w4", "pack_w4_from_simple", "pack_w8",
     "portable_layout", "quantize_w4_rtn", "quantize_w8_rtn", "register_layout", "repack", "roundup",
-    "sort_columns_by_group", "unpack_nibbles_int32", "unpack_w4", "unpack_w8",
+    "sort_columns_by_group", "unpack_nibbles_int32", "unpack_simple_int4", "unpack_w4", "unpack_w8",
 ]

@@ -101,3 +101,27 @@ def test_rtn_quantiser_bounds():
         deq = (q.float() - zz) * s[:, gi]
         assert q.max() <= 15 and (z is None) == sym
         assert (deq - w).abs().max() <= s.max() * 0.51 + 1e-6
+
+
+@pytest.mark.parametrize("n,k,gs,sym", [(37, 96, 32, False), (16, 256, 128, True), (9, 100, 8, False), (40, 64, -1, True)])
+def test_simple_int4_to_portable_is_bit_identical(n, k, gs, sym):
+    """forge.simple.v1 int4 (forge/formats/packing.py:1-5: element k in byte k // 2, even k = low nibble) converted to
+    portable_row equals pack_w4 of the same codes bit for bit; for K % 8 == 0 the weights are the same bytes."""
+    g = torch.Generator().manual_seed(n * k)
+    q = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8)
+    ng = L.num_groups(k, gs)
+    s = (torch.rand(n, ng, generator=g) * 0.02 + 0.001).half()
+    z = None if sym else torch.randint(0, 16, (n, ng), generator=g, dtype=torch.uint8)
+    simple = L.pack_simple_int4(q)
+    # the simple layout restated element by element
+    for (r, c) in [(0, 0), (0, 1), (n - 1, k - 1), (n // 2, 7)]:
+        assert (int(simple[r, c // 2]) >> (4 * (c % 2))) & 15 == int(q[r, c])
+    assert torch.equal(L.unpack_simple_int4(simple, k), q)
+    a = L.pack_w4_from_simple(simple, s, z, gs, k)
+    b = L.pack_w4(q, s, z, gs)
+    assert torch.equal(a.qweight, b.qweight) and torch.equal(a.scales, b.scales) and a.layout_id == b.layout_id
+    assert (a.zeros is None) == (b.zeros is None) and (a.zeros is None or torch.equal(a.zeros, b.zeros))
+    if k % 8 == 0:
+        assert a.qweight.data_ptr() == simple.data_ptr()  # a view, no copy
+    qq, ss, zz = L.unpack_w4(a)
+    assert torch.equal(qq, q) and torch.equal(ss, s) and (zz is None or torch.equal(zz, z))
