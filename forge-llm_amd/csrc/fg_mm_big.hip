@@ -4,8 +4,11 @@
 // registers per lane).  K is walked in 128-byte slices.  Each slice of A and B (2 x 32 KiB) is written straight from
 // global memory into one half of a double-buffered 128 KiB LDS ring by global_load_lds_dwordx4 (no staging registers,
 // no VALU), one wavefront instruction = 1 KiB = 8 rows x 128 bytes.  Within a 128-byte LDS row the 16-byte unit c of
-// global row r is stored at position c ^ (r & 7): the load lanes pick their global column so that this holds, and the
-// fragment reads (16 rows of one 16-row slab per instruction) then fall on 8 distinct bank groups.
+// global row r is stored at position c ^ key(r): the load lanes pick their global column so that this holds.  The key
+// makes the fragment reads (16 rows of one 16-row slab per instruction) free of LDS bank conflicts, as measured with
+// the SQ_LDS_BANK_CONFLICT counter on gfx950: r & 7 for the INT8 reads (unit 4 s + lane / 16 per lane), and
+// (r & 7) ^ ((r >> 3) & 1) for the FP8 reads (units 2 (lane / 16) and + 1), which conflict 4 cycles per instruction
+// under r & 7.
 //
 // Epilogue for 16-bit outputs: the fp32 result of each 16-row slab of a wavefront tile is scaled, rounded and written
 // to a per-wavefront LDS buffer, then stored as 16-byte row segments (row scales read once per row, column scales and
@@ -22,16 +25,20 @@ struct IsVec16 : std::false_type {};
 template <class E>
 struct IsVec16<E, std::void_t<decltype(E::kVec16)>> : std::integral_constant<bool, E::kVec16> {};
 
-// Fragment of row `rp` (one row of a 16-row slab, 128 bytes in LDS, units swizzled by r16 = row % 16) for k-step s.
+// Fragment of row `rp` (one row of a 16-row slab, 128 bytes in LDS, units swizzled by key(r16), r16 = row % 16) for
+// k-step s.
 struct MmaI8Big : MmaI8 {  // 16 bytes per lane: unit 4s + lane/16
+  static __device__ __forceinline__ int key(int r) { return r & 7; }
   static __device__ __forceinline__ frag_t load_sw(const uint8_t* rp, int r16, int lane, int s) {
-    const int c = (4 * s + (lane >> 4)) ^ (r16 & 7);
+    const int c = (4 * s + (lane >> 4)) ^ key(r16);
     return *reinterpret_cast<const i32x4*>(rp + c * 16);
   }
 };
 struct MmaF8Big : MmaF8 {  // 32 bytes per lane: units 2 * (lane/16) and +1 (one k-step per 128-byte slice)
+  static __device__ __forceinline__ int key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
   static __device__ __forceinline__ frag_t load_sw(const uint8_t* rp, int r16, int lane, int) {
-    const int c0 = (2 * (lane >> 4)) ^ (r16 & 7), c1 = (2 * (lane >> 4) + 1) ^ (r16 & 7);
+    const int k = key(r16);
+    const int c0 = (2 * (lane >> 4)) ^ k, c1 = (2 * (lane >> 4) + 1) ^ k;
     const i32x4 lo = *reinterpret_cast<const i32x4*>(rp + c0 * 16);
     const i32x4 hi = *reinterpret_cast<const i32x4*>(rp + c1 * 16);
     frag_t f;
@@ -101,20 +108,24 @@ __global__ void __launch_bounds__(kBigWM * kBigWN * 64) mm_big_kernel(const uint
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // Load instruction i of wave w fills LDS units (w * INSTR + i) * 64 + lane, i.e. row (w * INSTR + i) * 8 + lane / 8,
-  // position lane % 8, which holds global unit (lane % 8) ^ (row % 8) = (lane % 8) ^ (lane / 8).
-  const int lrow = lane >> 3, lcol = ((lane & 7) ^ (lane >> 3)) * 16;
+  // Load instruction i of wave w fills LDS units (w * INSTR + i) * 64 + lane, i.e. row r = (w * INSTR + i) * 8 +
+  // lane / 8, position lane % 8, which holds global unit (lane % 8) ^ key(r) (the swizzle is its own inverse).
+  const int lrow = lane >> 3;
   const int arow0 = wave * A_INSTR * 8 + lrow, brow0 = wave * B_INSTR * 8 + lrow;
   auto issue = [&](int kt, uint8_t* st) __attribute__((always_inline)) {
-    const int64_t ko = (int64_t)kt * BK + lcol;
+    const int64_t ko = (int64_t)kt * BK;
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i)
-      __builtin_amdgcn_global_load_lds(A + (int64_t)min(m0 + arow0 + 8 * i, M - 1) * lda + ko,
+    for (int i = 0; i < A_INSTR; ++i) {
+      const int col = ((lane & 7) ^ Mma::key(arow0 + 8 * i)) * 16;
+      __builtin_amdgcn_global_load_lds(A + (int64_t)min(m0 + arow0 + 8 * i, M - 1) * lda + ko + col,
                                        st + (wave * A_INSTR + i) * 1024, 16, 0, 0);
+    }
 #pragma unroll
-    for (int i = 0; i < B_INSTR; ++i)
-      __builtin_amdgcn_global_load_lds(B + (int64_t)min(n0 + brow0 + 8 * i, N - 1) * ldb + ko,
+    for (int i = 0; i < B_INSTR; ++i) {
+      const int col = ((lane & 7) ^ Mma::key(brow0 + 8 * i)) * 16;
+      __builtin_amdgcn_global_load_lds(B + (int64_t)min(n0 + brow0 + 8 * i, N - 1) * ldb + ko + col,
                                        st + BM * BK + (wave * B_INSTR + i) * 1024, 16, 0, 0);
+    }
   };
 
   typename Mma::acc_t acc[TM][TN];
