@@ -63,7 +63,8 @@ hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, 
                                 int K, int gs, bool single_group, hipStream_t s);
 bool w4_gemv_split_ok(int mt, int N, int K);
 bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
-                        int64_t lds, int N, int K);
+                             int64_t lds, int64_t ldq, const int32_t* zeros, int64_t ldz, int M, int N, int K, int gs,
+                             bool single_group);
 size_t w4_gemv_tile_lds_bytes(int mt, int K, int G, int TN);
 hipError_t launch_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
@@ -288,7 +289,8 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   hipError_t e;
   if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_AUTO) {
     // the split kernel in its branch-free form, else the tiled kernel, else whichever covers the shape
-    if (fg::w4_gemv_split_preferred(p.mt, x, ldx, perm, scales, scale_dtype, lds, (int)N, (int)K))
+    if (fg::w4_gemv_split_preferred(p.mt, x, ldx, perm, scales, scale_dtype, lds, ldq, zeros, ldz, (int)M, (int)N,
+                                    (int)K, gs, G == 1))
       p.gemv = FG_GEMV_SPLIT;
     else if (fg::w4_gemv_tile_ok(p.mt, (int)N, (int)K, (int)G, 0))
       p.gemv = FG_GEMV_TILE;

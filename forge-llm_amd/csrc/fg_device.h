@@ -161,6 +161,29 @@ __device__ __forceinline__ void tile_of(int bid, int ntm, int ntn, int& tm, int&
   tn = r / gsz;
 }
 
+// Raw buffer resource over `bytes` bytes from p (gfx9 dword3: 32-bit data format).  Loads through it take a per-lane
+// 32-bit voffset plus a wavefront-uniform soffset (a scalar register), need no 64-bit address math, and read 0 past the
+// end.  The caller guarantees bytes < 2^32.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes at voff + soff; the _nt form sets the non-temporal cache policy (data read once per call).
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (non-temporal: weights are read once per call and should not evict reusable lines)

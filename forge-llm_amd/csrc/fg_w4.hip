@@ -485,37 +485,56 @@ enum { kSplitGeneral = 0, kSplitF16Scales = 1, kSplitBf16Scales = 2 };  // w4_ge
 // from global memory next to the weights.  Every wavefront is independent until the final sum, so many of them per CU
 // keep HBM busy while others compute.
 // The FAST modes (N % R == 0, K % 32 == 0, fp16 or bf16 scales with lds % 8 == 0, 16-byte aligned x and scales,
-// ldx % 8 == 0, no perm; the scale type is a template parameter) issue every load of the wavefront unconditionally,
-// back to back, in the order of first use: a load under a branch, or a branch on the scale type between loads and
-// their use, makes the compiler wait for all earlier loads.  Symmetric weights then read a dummy word (`zeros` points
-// at any valid memory, ldz = 0) and replace it by 0x88888888.  The general form takes ragged N, K tails, fp32 scales,
+// ldx % 8 == 0, no perm, every operand spanning < 4 GiB; the scale type is a template parameter) issue every load of
+// the wavefront unconditionally, back to back, in the order of first use: a load under a branch, or a branch on the
+// scale type between loads and their use, makes the compiler wait for all earlier loads.  They are buffer loads: the
+// per-lane offset (the chunk) is one 32-bit value and the row parts, the same for the whole wavefront, go in scalar
+// registers, so a row costs no 64-bit address arithmetic.  Symmetric weights then read a dummy word (`zeros` points at
+// any valid memory, ldz = 0) and replace it by 0x88888888.  The general form takes ragged N, K tails, fp32 scales,
 // unaligned or permuted x with per-element loads.
 //   gs32: group size / 32 (groups are whole chunks), 0 for one group per row.
 // Threads per workgroup at most (BW * KS wavefronts): 512 for four rows of x, which need more than 128 registers.
 constexpr int w4_split_max_threads(int mt) { return mt == 4 ? 512 : 1024; }
 
+// Launch constants of the split GEMV, computed on the host so that the kernel prologue (run by every wavefront at the
+// same moment, on the CU's shared scalar unit) has no integer division before the loads go out.
+struct SplitArgs {
+  int KC;         // 32-column chunks of K
+  int cps;        // chunks per K slice (the last slice may be shorter)
+  int gs32;       // group size / 32, 0 for one group per row
+  uint32_t gmul;  // group of chunk c = umulhi(c, gmul) when gs32 > 1 (floor((2^32 - 1) / gs32) + 1)
+  uint32_t qbytes, xbytes, sbytes, zbytes;  // FAST: byte spans of qweight, x, scales, zeros (each < 2^32)
+};
+
+// Workgroup: blockDim.x = 64 * BW (one wavefront per channel block), blockDim.y = KS (one row of wavefronts per K
+// slice).
 template <int MT, int S, int R, bool XBF16, int MODE>
 __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ perm, const int32_t* __restrict__ qw,
     int64_t ldq, const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz,
     int hasz, const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
-    int gs32, int KS) {
+    SplitArgs a) {
   static_assert(R * MT == 4 || R * MT == 8 || R * MT == 16, "rows x batch must be 4, 8 or 16");
   constexpr bool FAST = MODE != kSplitGeneral;
   constexpr uint32_t kMagicBytes = XBF16 ? 0x43434343u : 0x64646464u;
   constexpr uint32_t kOnes = XBF16 ? 0x3f803f80u : 0x3c003c00u;  // (1, 1) as bf16 / fp16 pairs
   constexpr float kB = XBF16 ? 128.f : 1024.f;
   __shared__ float red[16][R * MT];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
-  const int BW = (int)(blockDim.x / kWave) / KS;
-  const int ks = wave % KS, blk = blockIdx.x * BW + wave / KS;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wb = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // channel block within the workgroup
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.y);         // K slice
+  const int BW = (int)(blockDim.x / kWave), KS = (int)blockDim.y;
+  const int KC = a.KC;
+  const int blk = blockIdx.x * BW + wb;
   const int n0 = blk * R;
   const int nr = min(n0, N - R);  // FAST: first row read (blocks past the end re-read the last block)
-  const int c0 = (int)((int64_t)ks * KC / KS), c1 = (int)((int64_t)(ks + 1) * KC / KS);
+  const int c0 = ks * a.cps, c1 = min(c0 + a.cps, KC);
   const int64_t ldq4 = ldq / 4;
   const uint4* __restrict__ qw4 = reinterpret_cast<const uint4*>(qw);
-  const FastDiv gdiv((uint32_t)max(gs32, 1));
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc(qw, a.qbytes);
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, a.xbytes);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(scales, a.sbytes);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(zeros, a.zbytes);
 
   int cl[S], gl[S];
   bool ok[S];
@@ -524,7 +543,7 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
     const int c = c0 + lane + kWave * i;
     ok[i] = c < c1;
     cl[i] = min(c, KC - 1);
-    gl[i] = gs32 > 0 ? (int)gdiv.div((uint32_t)cl[i]) : 0;
+    gl[i] = a.gs32 > 1 ? (int)__umulhi((uint32_t)cl[i], a.gmul) : (a.gs32 == 1 ? cl[i] : 0);
   }
   // Loads in the order of first use for one row of x: x (its chunk sums start every row), scales and zero words, then
   // the weights row by row (general form: rows past N re-read row N-1).  With 2-4 rows of x the weights go first:
@@ -540,7 +559,7 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
         for (int q = 0; q < 4; ++q) {
           const int wi = 4 * cl[i] + q;
           if constexpr (FAST) {
-            xv[m][i][q] = reinterpret_cast<const uint4*>(xr)[wi];
+            xv[m][i][q] = buf_ld16(rx, (uint32_t)cl[i] * 64u + 16u * q, (uint32_t)min(m, M - 1) * (uint32_t)ldx * 2u);
           } else {
             uint32_t h[8];
 #pragma unroll
@@ -559,24 +578,25 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int64_t srow = (int64_t)gl[i] * lds;
-      if constexpr (FAST) {
-        const uint16_t* sp = static_cast<const uint16_t*>(scales) + srow + nr;
+      if constexpr (FAST) {  // group row gl * lds (per lane, < 2^24 each) + the block's first channel (uniform)
+        const uint32_t sv = __umul24((uint32_t)gl[i], (uint32_t)lds) * 2u;
         if constexpr (R == 4) {
-          const uint2 t = *reinterpret_cast<const uint2*>(sp);
+          const uint2 t = buf_ld8(rs, sv, (uint32_t)nr * 2u);
           sraw[i][0] = t.x;
           sraw[i][1] = t.y;
         } else {
 #pragma unroll
           for (int h = 0; h < R / 8; ++h) {
-            const uint4 t = *reinterpret_cast<const uint4*>(sp + 8 * h);
+            const uint4 t = buf_ld16(rs, sv, (uint32_t)(nr + 8 * h) * 2u);
             sraw[i][4 * h] = t.x;
             sraw[i][4 * h + 1] = t.y;
             sraw[i][4 * h + 2] = t.z;
             sraw[i][4 * h + 3] = t.w;
           }
         }
+        const uint32_t zv = __umul24((uint32_t)gl[i], (uint32_t)ldz) * 4u;
 #pragma unroll
-        for (int h = 0; h < (R + 7) / 8; ++h) zw[i][h] = (uint32_t)zeros[(int64_t)gl[i] * ldz + nr / 8 + h];
+        for (int h = 0; h < (R + 7) / 8; ++h) zw[i][h] = buf_ld4(rz, zv, (uint32_t)(nr / 8 + h) * 4u);
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) sraw[i][r] = load_raw(scales, sdt, srow + min(n0 + r, N - 1));
@@ -587,12 +607,18 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
     }
   };
   uint4 w[R][S];
+  const uint32_t ldqb = (uint32_t)ldq * 4u;  // FAST: bytes per weight row
   auto load_w = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int i = 0; i < S; ++i)
-        w[r][i] = load16_stream(qw4 + (int64_t)(FAST ? nr + r : min(n0 + r, N - 1)) * ldq4 + cl[i]);
+      for (int i = 0; i < S; ++i) {
+        if constexpr (FAST) {
+          w[r][i] = buf_ld16_nt(rq, (uint32_t)cl[i] * 16u, (uint32_t)nr * ldqb + (uint32_t)r * ldqb);
+        } else {
+          w[r][i] = load16_stream(qw4 + (int64_t)min(n0 + r, N - 1) * ldq4 + cl[i]);
+        }
+      }
   };
   if constexpr (MT == 1) {
     load_x();
@@ -680,11 +706,11 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
   if (KS == 1) {
     if ((lane % span) == 0) store(lane / span, tot);
   } else {
-    if ((lane % span) == 0) red[wave][lane / span] = tot;
+    if ((lane % span) == 0) red[ks * BW + wb][lane / span] = tot;
     __syncthreads();
     if (ks == 0 && lane < R * MT) {  // the K slices of this block, summed in slice order
       float v = 0.f;
-      for (int k2 = 0; k2 < KS; ++k2) v += red[wave + k2][lane];
+      for (int k2 = 0; k2 < KS; ++k2) v += red[k2 * BW + wb][lane];
       store(lane, v);
     }
   }
@@ -726,12 +752,23 @@ static hipError_t launch_split_t(bool fast, const void* x, int64_t ldx, const in
   // symmetric weights: the zero word is read from qweight (always valid memory) and ignored
   const int32_t* zp = hasz ? zeros : qw;
   const int64_t ldzp = hasz ? ldz : 0;
-  const dim3 grid((nblk + BW - 1) / BW), block(kWave * BW * KS);
+  SplitArgs a;
+  a.KC = ((K + 7) / 8 + 3) / 4;
+  a.cps = (a.KC + KS - 1) / KS;
+  a.gs32 = gs32;
+  a.gmul = gs32 > 1 ? 0xffffffffu / (uint32_t)gs32 + 1u : 0u;
+  const int64_t G = gs32 > 0 ? (a.KC + gs32 - 1) / gs32 : 1;
+  // byte spans for the FAST buffer loads (split_fast checked each is < 2^32; unused by the general form)
+  a.qbytes = fast ? (uint32_t)((int64_t)N * ldq * 4) : 0u;
+  a.xbytes = fast ? (uint32_t)((int64_t)M * ldx * 2) : 0u;
+  a.sbytes = fast ? (uint32_t)(G * lds * 2) : 0u;
+  a.zbytes = fast ? (hasz ? (uint32_t)(G * ldz * 4) : a.qbytes) : 0u;
+  const dim3 grid((nblk + BW - 1) / BW), block(kWave * BW, KS);
   auto kern = !fast ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitGeneral>
                     : (sdt == FG_BF16 ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales>
                                       : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales>);
   hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const uint16_t*>(x), ldx, perm, qw, ldq, scales, sdt, lds, zp,
-                     ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gs32, KS);
+                     ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, a);
   return hipGetLastError();
 }
 
@@ -756,10 +793,14 @@ static hipError_t launch_split_x(int mt, int S, int R, bool fast, const void* x,
 
 // True when the split GEMV can take its branch-free form for these operands.
 static bool split_fast(int R, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
-                       int64_t lds, int N, int K) {
+                       int64_t lds, int64_t ldq, int64_t ldz, int M, int N, int K, int gs32) {
+  const int64_t KC = (K + 31) / 32, G = gs32 > 0 ? (KC + gs32 - 1) / gs32 : 1;
+  const int64_t lim = int64_t(1) << 32, lim24 = int64_t(1) << 24;  // buffer spans; 24-bit per-lane group offsets
   return perm == nullptr && (K % 32) == 0 && (N % R) == 0 && (ldx % 8) == 0 &&
          (reinterpret_cast<uintptr_t>(x) % 16) == 0 && sdt != FG_F32 && (lds % 8) == 0 &&
-         (reinterpret_cast<uintptr_t>(scales) % 16) == 0;
+         (reinterpret_cast<uintptr_t>(scales) % 16) == 0 && (int64_t)N * ldq * 4 < lim &&
+         (int64_t)M * ldx * 2 < lim && G * lds * 2 < lim && G * ldz * 4 < lim && lds < lim24 && ldz < lim24 &&
+         G < lim24;
 }
 
 hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
@@ -769,7 +810,7 @@ hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, 
   int S, R, KS, BW;
   if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return hipErrorInvalidValue;
   const int gs32 = single_group ? 0 : gs / 32;
-  const bool fast = split_fast(R, x, ldx, perm, scales, sdt, lds, N, K);
+  const bool fast = split_fast(R, x, ldx, perm, scales, sdt, lds, ldq, zeros ? ldz : 0, M, N, K, gs32);
   if (xbf16)
     return launch_split_x<true>(mt, S, R, fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy,
                                 M, N, K, gs32, KS, BW, s);
@@ -786,10 +827,12 @@ bool w4_gemv_split_ok(int mt, int N, int K) {
 // where the tiled kernel measured faster (3-4 rows of x over wide outputs: at K=4096, N=28672 the tiled kernel takes
 // 22 us against 28 us; at N=4096..6144 the split kernel is as fast or faster).
 bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
-                        int64_t lds, int N, int K) {
+                             int64_t lds, int64_t ldq, const int32_t* zeros, int64_t ldz, int M, int N, int K, int gs,
+                             bool single_group) {
   int S, R, KS, BW;
   if (mt == 4 && N / device_cus() >= 64) return false;
-  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW) && split_fast(R, x, ldx, perm, scales, sdt, lds, N, K);
+  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW) &&
+         split_fast(R, x, ldx, perm, scales, sdt, lds, ldq, zeros ? ldz : 0, M, N, K, single_group ? 0 : gs / 32);
 }
 
 // Generic kernel: any group size (multiple of 8), per-column g_idx, any ldq / alignment, any M.
