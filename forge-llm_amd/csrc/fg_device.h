@@ -1,9 +1,11 @@
-// Device-side helpers shared by the gfx950 kernels: number-format conversions, typed loads, wave reductions.
+// Helpers shared by the gfx950 kernels (number-format conversions, typed and buffer loads, wave reductions, tile
+// order) and by their host launchers (CU count, workgroup balance).
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/forge_mi355x.h"
@@ -203,6 +205,36 @@ __device__ __forceinline__ float raw_bits_to_f32(uint32_t raw, int dt) {
 // Element i of a 16- or 32-bit float array as raw bits (converted after the wait by raw_bits_to_f32).
 __device__ __forceinline__ uint32_t load_raw(const void* p, int dt, int64_t i) {
   return dt == FG_F32 ? static_cast<const uint32_t*>(p)[i] : (uint32_t) static_cast<const uint16_t*>(p)[i];
+}
+
+// ----------------------------------------------------------------------------------------------- host helpers
+// Compute units of the current device, queried once per device.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev < 0 || dev >= 64) dev = 0;
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
+// Channel blocks per workgroup (1, 2 or 4, with that many times ks wavefronts within maxw): the count whose workgroups
+// spread most evenly over the CUs, by busy fraction (workgroups / cus) / ceil(workgroups / cus) -- all are resident at
+// once, so 1.25 workgroups per CU take as long as 2 (measured 2x slower) -- the smallest on ties.
+inline int skinny_balance(int nblk, int ks, int maxw, int cus) {
+  int best = 1;
+  double best_eff = -1.0;
+  for (int bw = 1; bw <= 4 && bw * ks <= maxw; bw *= 2) {
+    const int wgs = (nblk + bw - 1) / bw;
+    const double per_cu = (double)wgs / cus;
+    const double eff = per_cu / ((wgs + cus - 1) / cus);
+    if (eff > best_eff + 1e-9) { best = bw; best_eff = eff; }
+  }
+  return best;
 }
 
 }  // namespace fg

@@ -1,14 +1,15 @@
 // Large-output W8A8 GEMMs (INT8 and FP8 e4m3fn), C[M,N] = A[M,K] @ B[N,K]^T with both operands K-contiguous.
 //
-// Workgroup tile 256 x 256, 512 threads = 2 x 4 wavefronts of 128 x 64 (8 x 4 MFMA tiles of 16 x 16, 128 accumulator
-// registers per lane).  K is walked in 128-byte slices.  Each slice of A and B (2 x 32 KiB) is written straight from
-// global memory into one half of a double-buffered 128 KiB LDS ring by global_load_lds_dwordx4 (no staging registers,
-// no VALU), one wavefront instruction = 1 KiB = 8 rows x 128 bytes.  Within a 128-byte LDS row the 16-byte unit c of
-// global row r is stored at position c ^ key(r): the load lanes pick their global column so that this holds.  The key
-// makes the fragment reads (16 rows of one 16-row slab per instruction) free of LDS bank conflicts, as measured with
-// the SQ_LDS_BANK_CONFLICT counter on gfx950: r & 7 for the INT8 reads (unit 4 s + lane / 16 per lane), and
-// (r & 7) ^ ((r >> 3) & 1) for the FP8 reads (units 2 (lane / 16) and + 1), which conflict 4 cycles per instruction
-// under r & 7.
+// Workgroup tile 256 x BN (BN = 256, or 320 for INT8 with 16-bit outputs where that fills the last round of
+// workgroups better), 512 threads = 2 x 4 wavefronts of 128 x BN/4 (8 x BN/64 MFMA tiles of 16 x 16, 128 or 160
+// accumulator registers per lane).  K is walked in 128-byte slices.  Each slice of A and B (32 KiB + BN/8 KiB) is
+// written straight from global memory into one half of a double-buffered LDS ring (128 or 144 KiB) by
+// global_load_lds_dwordx4 (no staging registers, no VALU), one wavefront instruction = 1 KiB = 8 rows x 128 bytes.
+// Within a 128-byte LDS row the 16-byte unit c of global row r is stored at position c ^ key(r): the load lanes pick
+// their global column so that this holds.  The key makes the fragment reads (16 rows of one 16-row slab per
+// instruction) free of LDS bank conflicts, as measured with the SQ_LDS_BANK_CONFLICT counter on gfx950: r & 7 for the
+// INT8 reads (unit 4 s + lane / 16 per lane), and (r & 7) ^ ((r >> 3) & 1) for the FP8 reads (units 2 (lane / 16)
+// and + 1), which conflict 4 cycles per instruction under r & 7.
 //
 // Epilogue for 16-bit outputs: the fp32 result of each 16-row slab of a wavefront tile is scaled, rounded and written
 // to a per-wavefront LDS buffer, then stored as 16-byte row segments (row scales read once per row, column scales and
@@ -87,13 +88,13 @@ struct EpiFp8V {
 };
 
 constexpr int kBigBM = 256, kBigBN = 256, kBigWM = 2, kBigWN = 4, kBigBK = 128;
-constexpr size_t kBigLds = 2 * (size_t)(kBigBM + kBigBN) * kBigBK;
+constexpr size_t big_lds_bytes(int bn) { return 2 * (size_t)(kBigBM + bn) * kBigBK; }
 
-template <class Mma, class Epi>
+template <class Mma, class Epi, int BN>
 __global__ void __launch_bounds__(kBigWM * kBigWN * 64) mm_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
                                                                       const uint8_t* __restrict__ B, int64_t ldb,
                                                                       int M, int N, int K, Epi epi) {
-  constexpr int BM = kBigBM, BN = kBigBN, WM = kBigWM, WN = kBigWN, BK = kBigBK;
+  constexpr int BM = kBigBM, WM = kBigWM, WN = kBigWN, BK = kBigBK;
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int A_INSTR = BM * BK / 16 / NT, B_INSTR = BN * BK / 16 / NT;  // 1 KiB load instructions per wave
@@ -185,9 +186,11 @@ __global__ void __launch_bounds__(kBigWM * kBigWN * 64) mm_big_kernel(const uint
         for (int e = 0; e < 4; ++e)
           slab[(4 * (lane >> 4) + e) * SP + j * 16 + (lane & 15)] = epi.cvt(epi.value(acc[i][j][e], rs[e], cs[j], cb[j]));
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's slab writes are done before it reads them
+      constexpr int NU = 16 * SW / 8;  // 16-byte units of the slab: 128 (BN = 256) or 160 (BN = 320)
 #pragma unroll
-      for (int u0 = 0; u0 < 16 * SW / 8; u0 += 64) {
+      for (int u0 = 0; u0 < NU; u0 += 64) {
         const int u = u0 + lane, r = u / (SW / 8), c8 = u % (SW / 8);
+        if (NU % 64 != 0 && u >= NU) break;  // the last pass of a 160-unit slab has 32 lanes of work
         const int m = mw + i * 16 + r, n = nw + c8 * 8;
         const uint4 v = *reinterpret_cast<const uint4*>(slab + r * SP + c8 * 8);
         if (m < M) {
@@ -224,16 +227,37 @@ bool mm_big_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t K
 // Workgroups of the 256 x 256 kernel for an M x N output.
 int64_t mm_big_tiles(int64_t M, int64_t N) { return ((M + kBigBM - 1) / kBigBM) * ((N + kBigBN - 1) / kBigBN); }
 
+// Tile width for an M x N output: 320 when its rounds of workgroups over the CUs, weighted by the tile width, cost
+// less than those of 256 (K=8192, N=10240, M=4096: 640 tiles of 256 take 3 rounds, the last half empty; 512 tiles of
+// 320 take 2).
+int mm_big_bn(int64_t M, int64_t N) {
+  const int64_t cus = device_cus(), tm = (M + kBigBM - 1) / kBigBM;
+  const int64_t r256 = (tm * ((N + 255) / 256) + cus - 1) / cus, r320 = (tm * ((N + 319) / 320) + cus - 1) / cus;
+  return r320 * 320 < r256 * 256 ? 320 : 256;
+}
+
+template <class Mma, int BN, class Epi>
+static hipError_t launch_big_t(const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, int M, int N, int K,
+                               const Epi& epi, hipStream_t s) {
+  auto k = mm_big_kernel<Mma, Epi, BN>;
+  constexpr size_t lds = big_lds_bytes(BN);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)lds);
+  if (e != hipSuccess) return e;
+  const unsigned tiles = (unsigned)(((M + kBigBM - 1) / kBigBM) * ((N + BN - 1) / BN));
+  hipLaunchKernelGGL(k, dim3(tiles), dim3(kBigWM * kBigWN * 64), lds, s, A, lda, B, ldb, M, N, K, epi);
+  return hipGetLastError();
+}
+
+// The 320-wide tile only for INT8 with 16-bit outputs: it takes 234 registers per lane there, and spills for FP8
+// fragments (8 registers each) or the element-wise 32-bit epilogue.
 template <class Mma, class Epi>
 static hipError_t launch_big(const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, int M, int N, int K,
                              const Epi& epi, hipStream_t s) {
-  auto k = mm_big_kernel<Mma, Epi>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)kBigLds);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3((unsigned)mm_big_tiles(M, N)), dim3(kBigWM * kBigWN * 64), kBigLds, s, A, lda, B, ldb, M,
-                     N, K, epi);
-  return hipGetLastError();
+  if constexpr (std::is_same<Mma, MmaI8Big>::value && IsVec16<Epi>::value) {
+    if (mm_big_bn(M, N) == 320) return launch_big_t<Mma, 320>(A, lda, B, ldb, M, N, K, epi, s);
+  }
+  return launch_big_t<Mma, 256>(A, lda, B, ldb, M, N, K, epi, s);
 }
 
 static bool vec16_ok(const void* y, int64_t ldy) { return ldy % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0; }

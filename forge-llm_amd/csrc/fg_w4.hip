@@ -473,7 +473,6 @@ __global__ void __launch_bounds__(w4_tile_max_waves(MT, S) * kWave) w4_gemv_tile
   }
 }
 
-static int device_cus();
 
 // ------------------------------------------------------------------------------------------------ GEMV (split-K)
 enum { kSplitGeneral = 0, kSplitF16Scales = 1, kSplitBf16Scales = 2 };  // w4_gemv_split_kernel MODE
@@ -947,16 +946,6 @@ hipError_t launch_w4_gemv(int mt, int R, bool xbf16, const void* x, int64_t ldx,
     FG_GEMV(4, false);
   }
 #undef FG_GEMV
-}
-
-static int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  }
-  return cus;
 }
 
 template <int MT, int S, bool XBF16>

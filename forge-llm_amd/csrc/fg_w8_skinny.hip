@@ -144,36 +144,11 @@ bool w8_skinny_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_
          M * lda < k4g && N * ldb < k4g;
 }
 
-static int w8sk_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  }
-  return cus;
-}
-
-// Channel blocks per workgroup (1, 2 or 4, at most maxw / ks wavefronts): the count whose workgroups spread most
-// evenly over the CUs (all resident at once, so 1.25 workgroups per CU take as long as 2: measured 2x slower), the
-// smallest on ties.
-static int skinny_balance(int nblk, int ks, int maxw, int cus) {
-  int best = 1;
-  double best_eff = -1.0;
-  for (int bw = 1; bw <= 4 && bw * ks <= maxw; bw *= 2) {
-    const int wgs = (nblk + bw - 1) / bw;
-    const double per_cu = (double)wgs / cus;
-    const double eff = per_cu / ((wgs + cus - 1) / cus);  // busy fraction of the CU-rounds
-    if (eff > best_eff + 1e-9) { best = bw; best_eff = eff; }
-  }
-  return best;
-}
-
 // Launch shape: T tiles of 16 channels per wavefront, the largest of 4 / 2 / 1 (2 for M <= 32, 1 for M <= 64: the x
 // registers) leaving at least 3/4 of a channel block per CU; KS K slices so that about 4 wavefronts per CU exist (at
 // most the workgroup limit and the 256-byte steps); two channel blocks per workgroup from 1.5 blocks per CU.
 void w8_skinny_plan(int M, int N, int K, int* mb, int* T, int* KS, int* BW) {
-  const int cus = w8sk_cus();
+  const int cus = device_cus();
   const int b = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   int t = b == 1 ? 4 : (b == 2 ? 2 : 1);
   while (t > 1 && 4 * ((N + 16 * t - 1) / (16 * t)) < 3 * cus) t /= 2;

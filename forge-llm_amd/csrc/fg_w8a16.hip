@@ -230,21 +230,11 @@ bool w8a16_skinny_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, 
          (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && N * ldq < k4g && M * ldx * 2 < k4g && G * lds * 2 < k4g;
 }
 
-static int w8a_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  }
-  return cus;
-}
-
 // Same shape rules as the W4 skinny kernel (the weight bytes per step double, the register budget is the same):
 // T tiles (4 / 2 / 1, capped by the rows of x) leaving at least 3/4 of a channel block per CU, 2-4 K slices, channel
 // blocks per workgroup chosen so that workgroups spread evenly over the CUs.
 static void w8a16_plan(int M, int N, int K, int* mb, int* T, int* KS, int* BW) {
-  const int cus = w8a_cus();
+  const int cus = device_cus();
   const int b = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   int t = b == 1 ? 4 : (b == 2 ? 2 : 1);
   while (t > 1 && 4 * ((N + 16 * t - 1) / (16 * t)) < 3 * cus) t /= 2;

@@ -85,6 +85,27 @@ def test_big_int8_full_size_matches_128_tiles(k, n):
     assert np.array_equal(y[rows].cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("n", [10240, 10203])
+def test_big_int8_wide_tiles_bf16(n):
+    """M=4096, N~10240: 640 tiles of 256 x 256 would fill 2.5 rounds of 256 CUs, so the policy runs 256 x 320 tiles
+    (2 rounds) for 16-bit outputs; the bf16 result equals the 128 x 128 kernel's bit for bit (same int32 accumulators,
+    same epilogue order), the ragged last tile included, and matches the oracle on sampled rows."""
+    g = torch.Generator(device=DEV).manual_seed(n)
+    a = torch.randint(-127, 128, (4096, 1024), dtype=torch.int8, device=DEV, generator=g)
+    w = torch.randint(-127, 128, (n, 1024), dtype=torch.int8, device=DEV, generator=g)
+    sa = torch.rand(4096, device=DEV, generator=g) * 0.01 + 0.001
+    sw = torch.rand(n, device=DEV, generator=g) * 0.01 + 0.001
+    b = torch.randn(n, device=DEV, generator=g)
+    y = ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16)
+    y128 = ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16, config={"tile_m": 128})
+    assert torch.equal(y, y128)
+    rows = [0, 1023, 2050, 4095]
+    xq, wq = a[rows].cpu().numpy(), w.cpu().numpy()
+    ref = og.int8_gemm_ref(xq, sa[rows].cpu().numpy(), wq, sw.cpu().numpy(), b.cpu().numpy(),
+                           acc=og.int8_matmul_exact(xq, wq))
+    assert torch.equal(y[rows].cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+
+
 def test_big_fp8_full_size_matches_128_tiles():
     """configs[3] at M=4096, K=N=8192 with bf16 output and per-token x per-channel scales."""
     g = torch.Generator(device=DEV).manual_seed(5)
