@@ -8,6 +8,7 @@
 #include <string>
 
 #include "../../include/forge_mi355x.h"
+#include "fg_device.h"
 
 namespace fg {
 hipError_t launch_w4_gemv(int mt, int R, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
@@ -124,22 +125,30 @@ bool is_float_dt(int dt) { return dt == FG_F32 || dt == FG_F16 || dt == FG_BF16;
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
 
-// W8A8 tile policy: tile_m = 256 (config or automatic) selects the 256 x 256 direct-to-LDS kernel, which needs
+// W8A8 tile policy: tile_m = 256 (config or automatic) selects the 256-row direct-to-LDS kernel, which needs
 // K % 128 == 0 and 16-byte aligned operands with 16-byte multiple leading dimensions; it is chosen automatically once
-// its tiles cover every CU of an MI355X (256) at least once.  Otherwise 64 x 64 (M or N <= 64) or 128 x 128 tiles.
-// Tile 16 selects the skinny kernel (M <= 64, K % 256 == 0, 16-byte aligned operands; register-resident split-K),
-// chosen automatically for M <= 64 where it applies.
-int mm_tile(int64_t M, int64_t N, int64_t K, const void* a, int64_t lda, const void* b, int64_t ldb,
+// its 256 x 256 tiles cover at least half the CUs.  Otherwise 64 x 64 (M or N <= 64) or 128 x 128 tiles.  Tile 16
+// selects the skinny kernel (M <= 64, K % 256 == 0, 16-byte aligned operands; register-resident split-K), chosen
+// automatically for M <= 64 where it applies and measured faster.
+int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t lda, const void* b, int64_t ldb,
             const fg_mm_config* cfg) {
   const bool big_ok = fg::mm_big_ok(a, lda, b, ldb, K);
   const bool skinny_ok = fg::w8_skinny_ok(a, lda, b, ldb, M, N, K);
   if (cfg && cfg->tile_m)
     return ((cfg->tile_m == 256 && !big_ok) || (cfg->tile_m == 16 && !skinny_ok)) ? -1 : cfg->tile_m;
-  // measured on the configs' shapes: the skinny kernel wins for M <= 16 below N = 32768 and for M <= 64 below
-  // N = 16384; 64-row tiles win while 128-row tiles would leave fewer than two per CU (fp8 M = 256: 538 against
-  // 381 TFLOP/s)
-  if (skinny_ok && N < 32768 && (M <= 16 || N < 16384)) return 16;
-  if (big_ok && fg::mm_big_tiles(M, N) >= 256) return 256;
+  // Measured on the configs' shapes (us, bf16 output):
+  //  * the skinny kernel wins for M <= 16 below N = 32768 and for M <= 64 below N = 16384, except INT8 at 33..64
+  //    rows with K < 16384, where the 64-row tiles read x fewer times (M=64, K=8192, N=10240: 47 against 66; at
+  //    K=28672, N=8192 the skinny kernel stays ahead, 131 against 147);
+  //  * the 256-row kernel wins once its tiles cover the CUs, and from half the CUs' worth with at least four tile
+  //    rows (fp8 M=1024, K=N=8192: 128 tiles, 88 against 105 for 128-row tiles; at M=512, 64 tiles, the 64-row tiles
+  //    are ahead, 77 against 86; one tile row over wide N, as M <= 64 at N=57344, wastes the tile: 120 against 101);
+  //  * 64-row tiles win while 128-row tiles would leave fewer than two per CU (fp8 M=256: 538 against 381 TFLOP/s).
+  if (skinny_ok && N < 32768 && (M <= 16 || N < 16384) && !(int8 && M > 32 && K < 16384)) return 16;
+  if (big_ok) {
+    const int64_t tiles = fg::mm_big_tiles(M, N), cus = fg::device_cus();
+    if (tiles >= cus || (M >= 1024 && 2 * tiles >= cus)) return 256;
+  }
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   return (M <= 64 || N <= 64 || tiles128 < 512) ? 64 : 128;
 }
@@ -427,7 +436,7 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
     if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad bias dtype");
   }
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
-  const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
+  const int tile = mm_tile(M, N, K, true, a, lda, b, ldb, cfg);
   if (tile < 0)
     return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
                                  "both 16-byte aligned operands");
@@ -458,7 +467,7 @@ int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (scale_mode == 0 || scale_mode == 1) {
     if (scale_mode == 0) sa_sm = sb_sn = 0;
-    const int tile = mm_tile(M, N, K, a, lda, b, ldb, cfg);
+    const int tile = mm_tile(M, N, K, false, a, lda, b, ldb, cfg);
     if (tile < 0)
       return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
                                    "both 16-byte aligned operands");
