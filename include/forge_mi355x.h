@@ -57,7 +57,8 @@ typedef struct fg_w4_config {
 } fg_w4_config;
 
 typedef struct fg_mm_config {
-  int32_t tile_m; /* 0 = policy; 64 / 128 = square tiles of that size; 256 = the 256 x 256 direct-to-LDS kernel
+  int32_t tile_m; /* 0 = policy; 64 / 128 = square tiles of that size; 256 = the 256-row direct-to-LDS kernel (256 x 256
+                     tiles, 256 x 320 for INT8 with 16-bit outputs where that fills the CUs' last round better)
                      (needs K % 128 == 0 and 16-byte aligned A, B with lda, ldb multiples of 16, else FG_EUNSUPPORTED);
                      16 = the skinny split-K kernel (M <= 64, K % 256 == 0, same alignment; modes 0 / 1) */
   int32_t tile_n;
