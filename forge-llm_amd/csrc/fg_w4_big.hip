@@ -64,7 +64,13 @@ __device__ __forceinline__ uint4 w4big_frag(const uint8_t* rp, int r16, int lane
 
 // WB = 4: packed int4 qweight (int32 words, ldq in words) with zero-points; WB = 8: int8 qweight (ldq in bytes),
 // symmetric (W8A16).
-template <int BM, bool XBF16, int WB>
+// PF2 (16-bit scales, K chunks of whole 128-column pairs of slices): the weights, scale and zero word of slice kt + 2
+// are fetched while slice kt's MFMAs run and slice kt + 1's are dequantised into LDS -- two register sets, the loop
+// unrolled by two with no branch in it -- so a slice's HBM latency is covered by two slices of work instead of one
+// (small M has little work per slice).  Every fetch is exactly three loads, issued after the slice's x loads (pinned by
+// sched_barrier), and the end-of-slice wait for the x loads leaves those three in flight.  Loads past the last slice
+// re-read it (clamped) into registers or into an LDS half no one reads again.
+template <int BM, bool XBF16, int WB, bool PF2>
 __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const void* __restrict__ qw, int64_t ldq,
     const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz, int hasz,
@@ -105,24 +111,38 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
   const uint4* __restrict__ wsrc =
       WB == 4 ? reinterpret_cast<const uint4*>(static_cast<const int32_t*>(qw) + (int64_t)wn_ * ldq) + whalf
               : reinterpret_cast<const uint4*>(static_cast<const int8_t*>(qw) + (int64_t)wn_ * ldq) + 2 * whalf;
-  const FastDiv gdiv((uint32_t)max(gs32, 1));
-  uint4 wreg, wreg2;
-  uint32_t sreg, zreg;
-  auto fetch_w = [&](int k0) __attribute__((always_inline)) {
-    const int c = (k0 >> 5) + whalf;  // 32-column chunk index
-    const int g = gs32 > 0 ? (int)gdiv.div((uint32_t)c) : 0;
-    if constexpr (WB == 4) {
-      wreg = load16_stream(wsrc + (k0 >> 5));
-    } else {
-      wreg = load16_stream(wsrc + (k0 >> 4));
-      wreg2 = load16_stream(wsrc + (k0 >> 4) + 1);
-    }
-    sreg = load_raw(scales, sdt, (int64_t)g * lds + wn_);
-    if constexpr (WB == 4) zreg = (uint32_t)zeros[(int64_t)g * ldz + (wn_ >> 3)];
+  // Branch-free group index, scale and zero-point (a uniform condition inside the loop would become a scalar branch,
+  // which splits the loop body and makes the compiler wait for every load at the join): group of chunk c =
+  // umulhi(c, gmul) | (c & gsel) (gs32 > 1: floor(c / gs32); gs32 == 1: c; one group: 0).
+  const uint32_t gmul = gs32 > 1 ? 0xffffffffu / (uint32_t)gs32 + 1u : 0u, gsel = gs32 == 1 ? 0xffffffffu : 0u;
+  const uint32_t zmask = hasz ? 0xffffffffu : 0u, sbf16 = sdt == FG_BF16 ? 0xffffffffu : 0u;
+  struct WRegs {  // one slice of this thread's weights, its group's scale and zero-point word
+    uint4 w, w2;
+    uint32_t s, z;
   };
-  auto stash_w = [&](uint8_t* st) __attribute__((always_inline)) {
-    const float s = raw_bits_to_f32(sreg, sdt);
-    uint8_t* rp = st + BM * ROW + wrow * ROW;
+  auto fetch_w = [&](int k0, WRegs& r) __attribute__((always_inline)) {
+    const uint32_t c = (uint32_t)((k0 >> 5) + whalf);  // 32-column chunk index
+    const int g = (int)(__umulhi(c, gmul) | (c & gsel));
+    if constexpr (WB == 4) {
+      r.w = load16_stream(wsrc + (k0 >> 5));
+    } else {
+      r.w = load16_stream(wsrc + (k0 >> 4));
+      r.w2 = load16_stream(wsrc + (k0 >> 4) + 1);
+    }
+    if constexpr (PF2) {  // fp16 / bf16 scales only (the launcher takes PF2 for no other)
+      r.s = static_cast<const uint16_t*>(scales)[(int64_t)g * lds + wn_];
+    } else {  // any scale type
+      r.s = load_raw(scales, sdt, (int64_t)g * lds + wn_);
+    }
+    if constexpr (WB == 4) r.z = (uint32_t)zeros[(int64_t)g * ldz + (wn_ >> 3)];
+  };
+  // wbase: the weight rows of an LDS half (its x rows come first)
+  auto stash_w = [&](uint8_t* wbase, const WRegs& r) __attribute__((always_inline)) {
+    const uint4 wreg = r.w, wreg2 = r.w2;
+    const uint32_t sreg = r.s, zreg = (r.z & zmask) | (0x88888888u & ~zmask);  // symmetric: zero-point 8
+    const uint32_t f16 = __float_as_uint(f16_bits_to_f32((uint16_t)sreg));
+    const float s = PF2 ? __uint_as_float(((sreg << 16) & sbf16) | (f16 & ~sbf16)) : raw_bits_to_f32(sreg, sdt);
+    uint8_t* rp = wbase + wrow * ROW;
     if constexpr (WB == 8) {  // 32 signed bytes: q * s exactly as the oracle's fp32 product, rounded once
       const uint32_t wd[8] = {wreg.x, wreg.y, wreg.z, wreg.w, wreg2.x, wreg2.y, wreg2.z, wreg2.w};
 #pragma unroll
@@ -136,7 +156,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       }
       return;
     }
-    const float z = hasz ? (float)nibble(zreg, wn_ & 7) : 8.f;
+    const float z = (float)nibble(zreg, wn_ & 7);
     const float c = -z * s;
     const uint32_t wd[4] = {wreg.x, wreg.y, wreg.z, wreg.w};
 #pragma unroll
@@ -165,21 +185,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_big_t{0.f, 0.f, 0.f, 0.f};
 
   const int r16 = lane & 15;
-  if (nk > 0) {
-    issue_x(kbeg, smem);
-    fetch_w(kbeg);
-    stash_w(smem);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* cur = smem + (kt & 1) * STAGE;
-    uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
-    const bool more = kt + 1 < nk;
-    if (more) {  // the other half of the ring is free since the last barrier
-      issue_x(kbeg + (kt + 1) * BK, nxt);
-      fetch_w(kbeg + (kt + 1) * BK);
-    }
+  auto mfma_slice = [&](const uint8_t* cur) __attribute__((always_inline)) {
     const uint8_t* sA = cur + (wm * TM * 16) * ROW;
     const uint8_t* sB = cur + BM * ROW + (wn * TN * 16) * ROW;
 #pragma unroll
@@ -194,9 +200,64 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
         for (int i = 0; i < TM; ++i) acc[i][j] = w4big_mfma<XBF16>(fa[i], fb, acc[i][j]);
       }
     }
-    if (more) stash_w(nxt);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next x slice landed in LDS
-    __syncthreads();                                  // ... for every wave; and this slice is no longer read
+  };
+  if constexpr (PF2) {
+    // Slice kt is in LDS half cur; rnext holds slice kt + 1; rfree is free.  The three regions are passed as
+    // __restrict__ pointers: the compiler otherwise cannot tell the x rows being loaded into the other half (LDS DMA)
+    // from the fragment reads of this half, or from the weight rows stored into the other half, and waits for every
+    // outstanding load -- the prefetch included -- before each of them.
+    auto body = [&](int kt, WRegs& rfree, const WRegs& rnext, const uint8_t* __restrict__ cur,
+                    uint8_t* __restrict__ nxt_x, uint8_t* __restrict__ nxt_w) __attribute__((always_inline)) {
+      issue_x(kbeg + min(kt + 1, nk - 1) * BK, nxt_x);  // that half is free since the last barrier
+      __builtin_amdgcn_sched_barrier(0);
+      fetch_w(kbeg + min(kt + 2, nk - 1) * BK, rfree);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_slice(cur);
+      __builtin_amdgcn_sched_barrier(0);  // keep the dequantisation (and its wait for rnext) after the MFMAs
+      stash_w(nxt_w, rnext);
+      // Slice kt + 1's x rows have landed (slice kt + 2's three loads may still be in flight) and this wave's LDS
+      // stores are done; then the workgroup barrier.  Not __syncthreads(): its release fence waits for every load,
+      // the prefetch included.  The memory clobber keeps the compiler from moving LDS accesses across it.
+      asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    WRegs ra, rb;
+    if (nk > 0) {
+      issue_x(kbeg, smem);
+      fetch_w(kbeg, ra);
+      stash_w(smem + BM * ROW, ra);
+      fetch_w(kbeg + min(1, nk - 1) * BK, rb);
+    }
+    asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    uint8_t* const h0 = smem;
+    uint8_t* const h1 = smem + STAGE;
+    for (int kt = 0; kt < nk; kt += 2) {  // nk is even (the host splits K in 128-column multiples)
+      body(kt, ra, rb, h0, h1, h1 + BM * ROW);
+      body(kt + 1, rb, ra, h1, h0, h0 + BM * ROW);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // the epilogue reuses the ring
+  } else {
+    WRegs rw;
+    if (nk > 0) {
+      issue_x(kbeg, smem);
+      fetch_w(kbeg, rw);
+      stash_w(smem + BM * ROW, rw);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
+      const bool more = kt + 1 < nk;
+      if (more) {  // the other half of the ring is free since the last barrier
+        issue_x(kbeg + (kt + 1) * BK, nxt);
+        fetch_w(kbeg + (kt + 1) * BK, rw);
+      }
+      mfma_slice(smem + (kt & 1) * STAGE);
+      __builtin_amdgcn_sched_barrier(0);  // keep the dequantisation (and its wait for the loads) after the MFMAs
+      if (more) stash_w(nxt + BM * ROW, rw);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next x slice landed in LDS
+      __syncthreads();                                  // ... for every wave; and this slice is no longer read
+    }
   }
 
   const int mw = m0 + wm * 16 * TM, nw = n0 + wn * 16 * TN;
@@ -272,7 +333,8 @@ void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kc
     if (s > 16) s = 16;
   }
   int kc = (K + s - 1) / s;
-  kc = (kc + kW4BigBK - 1) / kW4BigBK * kW4BigBK;
+  const int unit = K % (2 * kW4BigBK) == 0 ? 2 * kW4BigBK : kW4BigBK;  // whole slice pairs where K allows them
+  kc = (kc + unit - 1) / unit * unit;
   *kchunk = kc;
   *splits = (K + kc - 1) / kc;
 }
@@ -293,7 +355,11 @@ static hipError_t launch_w4_big_t(const void* x, int64_t ldx, const void* qw, in
                                   void* y, int64_t ldy, float* ws, int M, int N, int K, int gs32, int splits,
                                   int kchunk, hipStream_t s) {
   constexpr size_t shm = 2 * (size_t)(BM + kW4BigBN) * kW4BigBK * 2;
-  auto kern = w4_big_kernel<BM, XBF16, WB>;
+  // the two-slice-ahead form: 16-bit scales, and every K chunk an even number of slices (w4_big_plan rounds chunks to
+  // 128 columns when K allows)
+  // (64- and 128-row tiles: the 256-row one has no registers left for the second set)
+  const bool pf2 = BM <= 128 && sdt != FG_F32 && K % (2 * kW4BigBK) == 0;
+  auto kern = pf2 ? w4_big_kernel<BM, XBF16, WB, BM <= 128> : w4_big_kernel<BM, XBF16, WB, false>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)shm);
   if (e != hipSuccess) return e;
