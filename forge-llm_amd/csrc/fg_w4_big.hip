@@ -64,13 +64,15 @@ __device__ __forceinline__ uint4 w4big_frag(const uint8_t* rp, int r16, int lane
 
 // WB = 4: packed int4 qweight (int32 words, ldq in words) with zero-points; WB = 8: int8 qweight (ldq in bytes),
 // symmetric (W8A16).
-// PF2 (16-bit scales, K chunks of whole 128-column pairs of slices): the weights, scale and zero word of slice kt + 2
-// are fetched while slice kt's MFMAs run and slice kt + 1's are dequantised into LDS -- two register sets, the loop
-// unrolled by two with no branch in it -- so a slice's HBM latency is covered by two slices of work instead of one
-// (small M has little work per slice).  Every fetch is exactly three loads, issued after the slice's x loads (pinned by
-// sched_barrier), and the end-of-slice wait for the x loads leaves those three in flight.  Loads past the last slice
-// re-read it (clamped) into registers or into an LDS half no one reads again.
-template <int BM, bool XBF16, int WB, bool PF2>
+// PF (16-bit scales, K chunks of whole 128-column pairs of slices; PF = 0 otherwise): the loop is unrolled by two with
+// no branch in it, and the next slice's loads are issued before this slice's MFMAs, which no longer wait for them.
+// PF = 2 (64- and 128-row tiles): the weights, scale and zero word of slice kt + 2 are fetched while slice kt's MFMAs
+// run and slice kt + 1's are dequantised into LDS -- two register sets -- so a slice's HBM latency is covered by two
+// slices of work instead of one (small M has little work per slice); every fetch is exactly three loads, issued after
+// the slice's x loads (pinned by sched_barrier), and the end-of-slice wait for the x loads leaves those three in
+// flight.  PF = 1 (256-row tiles, no registers for a second set): slice kt + 1's weights load during slice kt's
+// MFMAs.  Loads past the last slice re-read it (clamped) into registers or into an LDS half no one reads again.
+template <int BM, bool XBF16, int WB, int PF>
 __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const void* __restrict__ qw, int64_t ldq,
     const void* __restrict__ scales, int sdt, int64_t lds, const int32_t* __restrict__ zeros, int64_t ldz, int hasz,
@@ -129,7 +131,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       r.w = load16_stream(wsrc + (k0 >> 4));
       r.w2 = load16_stream(wsrc + (k0 >> 4) + 1);
     }
-    if constexpr (PF2) {  // fp16 / bf16 scales only (the launcher takes PF2 for no other)
+    if constexpr (PF > 0) {  // fp16 / bf16 scales only (the launcher takes PF > 0 for no other)
       r.s = static_cast<const uint16_t*>(scales)[(int64_t)g * lds + wn_];
     } else {  // any scale type
       r.s = load_raw(scales, sdt, (int64_t)g * lds + wn_);
@@ -141,7 +143,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     const uint4 wreg = r.w, wreg2 = r.w2;
     const uint32_t sreg = r.s, zreg = (r.z & zmask) | (0x88888888u & ~zmask);  // symmetric: zero-point 8
     const uint32_t f16 = __float_as_uint(f16_bits_to_f32((uint16_t)sreg));
-    const float s = PF2 ? __uint_as_float(((sreg << 16) & sbf16) | (f16 & ~sbf16)) : raw_bits_to_f32(sreg, sdt);
+    const float s = PF > 0 ? __uint_as_float(((sreg << 16) & sbf16) | (f16 & ~sbf16)) : raw_bits_to_f32(sreg, sdt);
     uint8_t* rp = wbase + wrow * ROW;
     if constexpr (WB == 8) {  // 32 signed bytes: q * s exactly as the oracle's fp32 product, rounded once
       const uint32_t wd[8] = {wreg.x, wreg.y, wreg.z, wreg.w, wreg2.x, wreg2.y, wreg2.z, wreg2.w};
@@ -201,7 +203,9 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       }
     }
   };
-  if constexpr (PF2) {
+  uint8_t* const h0 = smem;
+  uint8_t* const h1 = smem + STAGE;
+  if constexpr (PF == 2) {
     // Slice kt is in LDS half cur; rnext holds slice kt + 1; rfree is free.  The three regions are passed as
     // __restrict__ pointers: the compiler otherwise cannot tell the x rows being loaded into the other half (LDS DMA)
     // from the fragment reads of this half, or from the weight rows stored into the other half, and waits for every
@@ -228,13 +232,37 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       fetch_w(kbeg + min(1, nk - 1) * BK, rb);
     }
     asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    uint8_t* const h0 = smem;
-    uint8_t* const h1 = smem + STAGE;
     for (int kt = 0; kt < nk; kt += 2) {  // nk is even (the host splits K in 128-column multiples)
       body(kt, ra, rb, h0, h1, h1 + BM * ROW);
       body(kt + 1, rb, ra, h1, h0, h0 + BM * ROW);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // the epilogue reuses the ring
+  } else if constexpr (PF == 1) {
+    // as PF = 2 with one register set: the loads of slice kt + 1 go out before slice kt's MFMAs, the weights are
+    // dequantised after them, and the slice ends once everything has landed
+    auto body = [&](int kt, WRegs& rw, const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt_x,
+                    uint8_t* __restrict__ nxt_w) __attribute__((always_inline)) {
+      const int kn = kbeg + min(kt + 1, nk - 1) * BK;
+      issue_x(kn, nxt_x);  // that half is free since the last barrier
+      fetch_w(kn, rw);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_slice(cur);
+      __builtin_amdgcn_sched_barrier(0);  // keep the dequantisation (and its wait for rw) after the MFMAs
+      stash_w(nxt_w, rw);
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    WRegs rw;
+    if (nk > 0) {
+      issue_x(kbeg, smem);
+      fetch_w(kbeg, rw);
+      stash_w(smem + BM * ROW, rw);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int kt = 0; kt < nk; kt += 2) {  // nk is even (the host splits K in 128-column multiples)
+      body(kt, rw, h0, h1, h1 + BM * ROW);
+      body(kt + 1, rw, h1, h0, h0 + BM * ROW);
+    }
     __syncthreads();  // the epilogue reuses the ring
   } else {
     WRegs rw;
@@ -355,11 +383,11 @@ static hipError_t launch_w4_big_t(const void* x, int64_t ldx, const void* qw, in
                                   void* y, int64_t ldy, float* ws, int M, int N, int K, int gs32, int splits,
                                   int kchunk, hipStream_t s) {
   constexpr size_t shm = 2 * (size_t)(BM + kW4BigBN) * kW4BigBK * 2;
-  // the two-slice-ahead form: 16-bit scales, and every K chunk an even number of slices (w4_big_plan rounds chunks to
-  // 128 columns when K allows)
-  // (64- and 128-row tiles: the 256-row one has no registers left for the second set)
-  const bool pf2 = BM <= 128 && sdt != FG_F32 && K % (2 * kW4BigBK) == 0;
-  auto kern = pf2 ? w4_big_kernel<BM, XBF16, WB, BM <= 128> : w4_big_kernel<BM, XBF16, WB, false>;
+  // the unrolled forms: 16-bit scales, and every K chunk an even number of slices (w4_big_plan rounds chunks to 128
+  // columns when K allows); two register sets for 64- and 128-row tiles, one for 256 (no registers left)
+  const bool pf = sdt != FG_F32 && K % (2 * kW4BigBK) == 0;
+  constexpr int kPf = BM <= 128 ? 2 : 1;
+  auto kern = pf ? w4_big_kernel<BM, XBF16, WB, kPf> : w4_big_kernel<BM, XBF16, WB, 0>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)shm);
   if (e != hipSuccess) return e;
