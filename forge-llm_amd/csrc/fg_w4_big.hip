@@ -161,9 +161,13 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     const float z = (float)nibble(zreg, wn_ & 7);
     const float c = -z * s;
     const uint32_t wd[4] = {wreg.x, wreg.y, wreg.z, wreg.w};
+    // The nibble mask is hidden from known-bits analysis: with it visible, byte k of a masked word (at most 15) is
+    // extracted with v_bfe_u32 and then converted, instead of converted directly by v_cvt_f32_ubyte{k}.
+    uint32_t nmask = 0x0F0F0F0Fu;
+    asm("" : "+v"(nmask));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // word i = columns 8 i .. 8 i + 7 of this thread's 32 = LDS unit 4 whalf + i
-      const uint32_t lo = wd[i] & 0x0F0F0F0Fu, hi = (wd[i] >> 4) & 0x0F0F0F0Fu;  // nibbles 0,2,4,6 / 1,3,5,7
+      const uint32_t lo = wd[i] & nmask, hi = (wd[i] >> 4) & nmask;  // nibbles 0,2,4,6 / 1,3,5,7
       float d[8];
       d[0] = __builtin_fmaf(ubyte_f32(lo, 0), s, c);
       d[1] = __builtin_fmaf(ubyte_f32(hi, 0), s, c);
@@ -210,6 +214,10 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     // __restrict__ pointers: the compiler otherwise cannot tell the x rows being loaded into the other half (LDS DMA)
     // from the fragment reads of this half, or from the weight rows stored into the other half, and waits for every
     // outstanding load -- the prefetch included -- before each of them.
+    //
+    // With a direct-to-LDS load in flight the compiler waits for every outstanding load (vmcnt(0)) before the first
+    // use of any register load, so every other slice's dequantisation waits for the loads issued at its top; the
+    // other slice's data is already covered by that wait.
     auto body = [&](int kt, WRegs& rfree, const WRegs& rnext, const uint8_t* __restrict__ cur,
                     uint8_t* __restrict__ nxt_x, uint8_t* __restrict__ nxt_w) __attribute__((always_inline)) {
       issue_x(kbeg + min(kt + 1, nk - 1) * BK, nxt_x);  // that half is free since the last barrier
