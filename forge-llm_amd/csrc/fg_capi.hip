@@ -88,6 +88,13 @@ hipError_t launch_int8_gemm_big(const int8_t* a, int64_t lda, const float* sa, i
 hipError_t launch_fp8_gemm_big(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
                                int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
                                int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
+int mm_ring_bn(int64_t M, int64_t N, int bm);
+hipError_t launch_int8_gemm_ring(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                                 int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                                 int64_t ldy, int ydt, int M, int N, int K, int bm, int bn, hipStream_t s);
+hipError_t launch_fp8_gemm_ring(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, const uint8_t* b,
+                                int64_t ldb, const float* sb, int64_t sb_sn, const void* bias, int bdt, void* y,
+                                int64_t ldy, int ydt, int M, int N, int K, int bm, int bn, hipStream_t s);
 hipError_t launch_fp8_gemm_blocked(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, int64_t sa_sk,
                                    const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_sn, int64_t sb_sk,
                                    int sb_div, const void* bias, int bdt, void* y, int64_t ldy, int ydt, int M, int N,
@@ -125,30 +132,47 @@ bool is_float_dt(int dt) { return dt == FG_F32 || dt == FG_F16 || dt == FG_BF16;
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
 
-// W8A8 tile policy: tile_m = 256 (config or automatic) selects the 256-row direct-to-LDS kernel, which needs
-// K % 128 == 0 and 16-byte aligned operands with 16-byte multiple leading dimensions; it is chosen automatically once
-// its 256 x 256 tiles cover at least half the CUs.  Otherwise 64 x 64 (M or N <= 64) or 128 x 128 tiles.  Tile 16
-// selects the skinny kernel (M <= 64, K % 256 == 0, 16-byte aligned operands; register-resident split-K), chosen
-// automatically for M <= 64 where it applies and measured faster.
+// W8A8 tile policy.  tile_m = 256 (config or automatic) selects the 256-row direct-to-LDS kernel; tile_m = 64 / 128
+// select 64- / 128-row tiles: the ring kernel (direct-to-LDS loads, several slices in flight) wherever the 256-row
+// kernel's conditions hold (K % 128 == 0, 16-byte aligned operands with 16-byte multiple leading dimensions), with
+// tile_n (32, 64, 128; 128 only for 128-row tiles) or mm_ring_bn choosing the width, else the register-staged tiled
+// kernel with square tiles.  Tile 16 selects the skinny kernel (M <= 64, K % 256 == 0, same alignment;
+// register-resident split-K).  Returns the tile (16, 64, 128, 256) and sets *ring when the ring kernel runs; -1 for a
+// configuration the operands do not allow.
 int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t lda, const void* b, int64_t ldb,
-            const fg_mm_config* cfg) {
+            const fg_mm_config* cfg, bool* ring) {
   const bool big_ok = fg::mm_big_ok(a, lda, b, ldb, K);
   const bool skinny_ok = fg::w8_skinny_ok(a, lda, b, ldb, M, N, K);
-  if (cfg && cfg->tile_m)
-    return ((cfg->tile_m == 256 && !big_ok) || (cfg->tile_m == 16 && !skinny_ok)) ? -1 : cfg->tile_m;
-  // Measured on the configs' shapes (us, bf16 output):
-  //  * the skinny kernel wins for M <= 16 below N = 32768 and for M <= 64 below N = 16384, except INT8 at 33..64
-  //    rows with K < 16384, where the 64-row tiles read x fewer times (M=64, K=8192, N=10240: 47 against 66; at
-  //    K=28672, N=8192 the skinny kernel stays ahead, 131 against 147);
-  //  * the 256-row kernel wins once its tiles cover the CUs, and from half the CUs' worth with at least four tile
-  //    rows (fp8 M=1024, K=N=8192: 128 tiles, 88 against 105 for 128-row tiles; at M=512, 64 tiles, the 64-row tiles
-  //    are ahead, 77 against 86; one tile row over wide N, as M <= 64 at N=57344, wastes the tile: 120 against 101);
-  //  * 64-row tiles win while 128-row tiles would leave fewer than two per CU (fp8 M=256: 538 against 381 TFLOP/s).
-  if (skinny_ok && N < 32768 && (M <= 16 || N < 16384) && !(int8 && M > 32 && K < 16384)) return 16;
+  *ring = false;
+  if (cfg && cfg->tile_m) {
+    const int t = cfg->tile_m, tn = cfg->tile_n;
+    if ((t == 256 && !big_ok) || (t == 16 && !skinny_ok)) return -1;
+    if (t == 64 || t == 128) {
+      if (tn && (!big_ok || (t == 64 && tn != 32 && tn != 64 && tn != 128) || (t == 128 && tn != 128))) return -1;
+      *ring = big_ok;
+    }
+    return t;
+  }
   if (big_ok) {
+    // Measured on the configs' shapes (us, bf16 output, random operands):
+    //  * the skinny kernel only for M <= 16 at K >= 16384 (int8 K=28672, N=8192: 45 / 56 at M = 1 / 16 against 58 /
+    //    60 for the ring kernel); at K = 8192 the ring kernel is ahead from M = 1 (int8 N=10240: 20 against 27; fp8
+    //    N=8192 at M=16: 17 against 19; int8 N=57344: 96 against 112), and at M = 32..64 everywhere (int8 K=28672,
+    //    M=64: 63 against 139);
+    //  * the 256-row kernel once its tiles cover the CUs, and from half the CUs' worth with M >= 1024 (fp8 M=1024,
+    //    K=N=8192: 128 tiles, 88 against 105 for 128-row register-staged tiles);
+    //  * below that the ring kernel: 128-row tiles once they number 5/8 of the CUs (fp8 M=512: 256 tiles, 47 against
+    //    62 for 64 x 128), else 64-row tiles (fp8 M=256: 33 against 65 for the register-staged 64 x 64 tiles).
+    if (skinny_ok && M <= 16 && K >= 16384) return 16;
     const int64_t tiles = fg::mm_big_tiles(M, N), cus = fg::device_cus();
     if (tiles >= cus || (M >= 1024 && 2 * tiles >= cus)) return 256;
+    *ring = true;
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    return (M > 64 && 8 * t128 >= 5 * cus) ? 128 : 64;
   }
+  // Unaligned operands or K % 128 != 0: the skinny kernel where it applies and was measured faster, else the
+  // register-staged tiles (64-row while 128-row tiles would leave fewer than two per CU).
+  if (skinny_ok && N < 32768 && (M <= 16 || N < 16384) && !(int8 && M > 32 && K < 16384)) return 16;
   const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
   return (M <= 64 || N <= 64 || tiles128 < 512) ? 64 : 128;
 }
@@ -436,10 +460,19 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
     if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad bias dtype");
   }
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
-  const int tile = mm_tile(M, N, K, true, a, lda, b, ldb, cfg);
+  bool ring;
+  const int tile = mm_tile(M, N, K, true, a, lda, b, ldb, cfg, &ring);
   if (tile < 0)
     return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
-                                 "both 16-byte aligned operands");
+                                 "both 16-byte aligned operands; tile_n (32, 64, 128 for tile_m=64, 128 for "
+                                 "tile_m=128) the same");
+  if (ring) {
+    const int bn = cfg && cfg->tile_n ? cfg->tile_n : fg::mm_ring_bn(M, N, tile);
+    return hip_status(fg::launch_int8_gemm_ring(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy,
+                                                y_dtype, (int)M, (int)N, (int)K, tile, bn,
+                                                static_cast<hipStream_t>(stream)),
+                      "fg_int8_gemm launch");
+  }
   if (tile == 16)
     return hip_status(fg::launch_int8_gemm_skinny(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy,
                                                   y_dtype, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream)),
@@ -467,10 +500,18 @@ int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (scale_mode == 0 || scale_mode == 1) {
     if (scale_mode == 0) sa_sm = sb_sn = 0;
-    const int tile = mm_tile(M, N, K, false, a, lda, b, ldb, cfg);
+    bool ring;
+    const int tile = mm_tile(M, N, K, false, a, lda, b, ldb, cfg, &ring);
     if (tile < 0)
       return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
-                                   "both 16-byte aligned operands");
+                                   "both 16-byte aligned operands; tile_n (32, 64, 128 for tile_m=64, 128 for "
+                                   "tile_m=128) the same");
+    if (ring) {
+      const int bn = cfg && cfg->tile_n ? cfg->tile_n : fg::mm_ring_bn(M, N, tile);
+      return hip_status(fg::launch_fp8_gemm_ring(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy,
+                                                 y_dtype, (int)M, (int)N, (int)K, tile, bn, s),
+                        "fg_fp8_gemm launch");
+    }
     if (tile == 16)
       return hip_status(fg::launch_fp8_gemm_skinny(a, lda, sa, sa_sm, b, ldb, sb, sb_sn, bias, bias_dtype, y, ldy,
                                                    y_dtype, (int)M, (int)N, (int)K, s),

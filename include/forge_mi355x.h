@@ -57,11 +57,14 @@ typedef struct fg_w4_config {
 } fg_w4_config;
 
 typedef struct fg_mm_config {
-  int32_t tile_m; /* 0 = policy; 64 / 128 = square tiles of that size; 256 = the 256-row direct-to-LDS kernel (256 x 256
-                     tiles, 256 x 320 for INT8 with 16-bit outputs where that fills the CUs' last round better)
-                     (needs K % 128 == 0 and 16-byte aligned A, B with lda, ldb multiples of 16, else FG_EUNSUPPORTED);
-                     16 = the skinny split-K kernel (M <= 64, K % 256 == 0, same alignment; modes 0 / 1) */
-  int32_t tile_n;
+  int32_t tile_m; /* 0 = policy; 64 / 128 = 64- / 128-row tiles: with K % 128 == 0 and 16-byte aligned A, B whose
+                     lda, ldb are multiples of 16, the ring kernel (direct-to-LDS loads, several K slices in flight;
+                     width from tile_n or the policy), otherwise square register-staged tiles; 256 = the 256-row
+                     direct-to-LDS kernel (256 x 256 tiles, 256 x 320 for INT8 with 16-bit outputs where that fills
+                     the CUs' last round better) (needs the same K and alignment, else FG_EUNSUPPORTED); 16 = the
+                     skinny split-K kernel (M <= 64, K % 256 == 0, same alignment; modes 0 / 1) */
+  int32_t tile_n; /* ring kernel tile width: 32, 64 or 128 with tile_m = 64, 128 with tile_m = 128 (needs the ring
+                     kernel's conditions, else FG_EUNSUPPORTED); 0 = policy; ignored for tile_m 16 / 256 */
   int32_t reserved[6];
 } fg_mm_config;
 

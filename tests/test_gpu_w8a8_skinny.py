@@ -1,6 +1,7 @@
 """GPU parity of the skinny W8A8 kernel (fg_w8_skinny.hip, M <= 64, register-resident split-K): INT8 accumulator and
 fp32 / bf16 / fp16 epilogues bit-exact against the CPU oracle (the int32 partials of the K slices sum exactly), FP8
-within the north-star bar and against the 64-row tiled kernel; forced with tile_m=16 and chosen by the policy."""
+within the north-star bar, as is the 64-row kernel on the same inputs; forced with tile_m=16, and the policy's own choice
+(the skinny kernel for M <= 16 at K >= 16384, the ring kernel for the other aligned shapes) held to the same bar."""
 from __future__ import annotations
 
 import numpy as np
@@ -39,7 +40,7 @@ def test_skinny_int8_exact_vs_oracle(m, n, k):
     ref32 = og.int8_gemm_ref(xq, sx, wq, sw, b.numpy(), acc=ref_acc)
     assert np.array_equal(y32, ref32)
     for odt in (torch.bfloat16, torch.float16):
-        y16 = ops.int8_gemm(a, ta, w, tb, b.to(DEV), out_dtype=odt).cpu()  # policy: skinny for these shapes
+        y16 = ops.int8_gemm(a, ta, w, tb, b.to(DEV), out_dtype=odt).cpu()  # the policy's kernel
         assert torch.equal(y16, torch.from_numpy(ref32).to(odt)), odt
 
 
