@@ -162,15 +162,13 @@ static hipError_t launch_mm(const uint8_t* A, int64_t lda, const uint8_t* B, int
   const bool aligned = (lda % 16 == 0) && (ldb % 16 == 0) && (K % 16 == 0) &&
                        ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16 == 0);
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  if (aligned) {
-    auto k = mm_kernel<Mma, TM, TN, true, Epi>;
-    if (shm > 64 * 1024) hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    hipLaunchKernelGGL(k, dim3(tiles), dim3(256), shm, s, A, lda, B, ldb, M, N, K, epi);
-  } else {
-    auto k = mm_kernel<Mma, TM, TN, false, Epi>;
-    if (shm > 64 * 1024) hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-    hipLaunchKernelGGL(k, dim3(tiles), dim3(256), shm, s, A, lda, B, ldb, M, N, K, epi);
+  auto k = aligned ? mm_kernel<Mma, TM, TN, true, Epi> : mm_kernel<Mma, TM, TN, false, Epi>;
+  if (shm > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
   }
+  hipLaunchKernelGGL(k, dim3(tiles), dim3(256), shm, s, A, lda, B, ldb, M, N, K, epi);
   return hipGetLastError();
 }
 

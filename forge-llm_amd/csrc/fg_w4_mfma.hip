@@ -253,7 +253,11 @@ static hipError_t launch_w4_mfma_t(const void* x, int64_t ldx, const int32_t* qw
   constexpr int BM = WM * TM * 16, BN = WN * TN * 16, PITCH = 64 * 2 + 16;
   const size_t shm = 2 * (size_t)(BM + BN) * PITCH;
   auto kern = w4_mfma_kernel<WM, WN, TM, TN, XBF16>;
-  if (shm > 64 * 1024) hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  if (shm > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   int kchunk = 0, used = 0;
   w4_mfma_split_plan(M, N, K, BM, splits, &kchunk, &used);
