@@ -71,6 +71,20 @@ def test_ring_fp8_vs_oracle_all_instances_equal(m, n, k):
     assert_close(y0.cpu(), ref0, "float32", what="fp8 ring per-tensor")
 
 
+@pytest.mark.parametrize("cfg", RINGS, ids=lambda c: f"{c['tile_m']}x{c['tile_n']}")
+def test_ring_int8_row_strided_x(cfg):
+    """x as a view into wider rows (lda = K + 128): rows are addressed through lda, not K."""
+    m, n, k = 70, 300, 640
+    xq, sx, wq, sw = _i8(m, n, k, seed=5)
+    wide = torch.full((m, k + 128), 99, dtype=torch.int8)
+    wide[:, :k] = torch.from_numpy(xq)
+    a = wide.to(DEV)[:, :k]
+    assert a.stride(0) == k + 128
+    w = torch.from_numpy(wq).to(DEV)
+    acc = ops.int8_gemm(a, None, w, None, out_dtype=torch.int32, config=cfg).cpu().numpy()
+    assert np.array_equal(acc, og.int8_matmul_exact(xq, wq))
+
+
 def test_ring_config_rejects():
     a = torch.zeros(8, 1000, dtype=torch.int8, device=DEV)
     w = torch.zeros(64, 1000, dtype=torch.int8, device=DEV)
