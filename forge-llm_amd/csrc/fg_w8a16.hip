@@ -242,14 +242,7 @@ static void w8a16_plan(int M, int N, int K, int* mb, int* T, int* KS, int* BW) {
   const int maxw = w8a16_max_threads(b, t) / kWave;
   int ks = (b == 1 && t <= 2) ? 4 : 2;
   ks = max(1, min(ks, K / 128));
-  int best = 1;
-  double best_eff = -1.0;
-  for (int bw = 1; bw <= 4 && bw * ks <= maxw; bw *= 2) {
-    const int wgs = (nblk + bw - 1) / bw;
-    const double eff = ((double)wgs / cus) / ((wgs + cus - 1) / cus);
-    if (eff > best_eff + 1e-9) { best = bw; best_eff = eff; }
-  }
-  *mb = b; *T = t; *KS = ks; *BW = best;
+  *mb = b; *T = t; *KS = ks; *BW = skinny_balance(nblk, ks, maxw, cus);
 }
 
 template <int MB, int T, bool XBF16, bool SBF16>
