@@ -320,6 +320,13 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
+  // 3-4 rows over weights larger than 4096 x 4096: the skinny MFMA kernel where it applies (it needs no workspace).
+  // Measured at M = 4 (us): qkv 8.2 against 8.7 for the GEMV, gate+up 20.5 against 22.8, down 14.8 against 16.2;
+  // o_proj (4096 x 4096) 6.8 against 6.1 stays on the GEMV, as do 1-2 rows.
+  if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_AUTO && (!cfg || cfg->impl == FG_W4_AUTO) && M > 2 &&
+      N * K > 4096LL * 4096 &&
+      fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G))
+    p.impl = FG_W4_MFMA;
   if (p.impl == FG_W4_GEMV && p.gemv == FG_GEMV_AUTO) {
     // the split kernel in its branch-free form, else the tiled kernel, else whichever covers the shape
     if (fg::w4_gemv_split_preferred(p.mt, x, ldx, perm, scales, scale_dtype, lds, ldq, zeros, ldz, (int)M, (int)N,
