@@ -74,7 +74,8 @@ __global__ void __launch_bounds__(w8_skinny_max_threads(MB, T)) w8_skinny_kernel
 #pragma unroll
   for (int t = 0; t < T; ++t) boff[t] = (uint32_t)min(n0 + 16 * t + r16, N - 1) * (uint32_t)ldb + 64u * j;
 #pragma unroll
-  for (int i = 0; i < MB; ++i) aoff[i] = (uint32_t)min(16 * i + r16, M - 1) * (uint32_t)lda + 64u * j;
+  for (int i = 0; i < MB; ++i)  // rows past M start at the end of A: their loads read 0 and fetch nothing
+    aoff[i] = 16 * i + r16 < M ? (uint32_t)(16 * i + r16) * (uint32_t)lda + 64u * j : (uint32_t)M * (uint32_t)lda;
 
   struct Buf {
     uint4 a[MB][4], b[T][4];

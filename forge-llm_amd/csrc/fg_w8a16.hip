@@ -85,7 +85,8 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
   }
   uint32_t xoff[MB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) xoff[i] = (uint32_t)min(16 * i + r16, M - 1) * (uint32_t)ldx * 2u + 64u * j;
+  for (int i = 0; i < MB; ++i)  // rows past M start at the end of x: their loads read 0 and fetch nothing
+    xoff[i] = 16 * i + r16 < M ? (uint32_t)(16 * i + r16) * (uint32_t)ldx * 2u + 64u * j : (uint32_t)M * (uint32_t)ldx * 2u;
   const FastDiv gdiv((uint32_t)max(gsteps, 1));
   const uint32_t lds32 = (uint32_t)lds;
 
