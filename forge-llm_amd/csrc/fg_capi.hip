@@ -159,13 +159,14 @@ int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t l
     //    60 for the ring kernel); at K = 8192 the ring kernel is ahead from M = 1 (int8 N=10240: 20 against 27; fp8
     //    N=8192 at M=16: 17 against 19; int8 N=57344: 96 against 112), and at M = 32..64 everywhere (int8 K=28672,
     //    M=64: 63 against 139);
-    //  * the 256-row kernel once its tiles cover the CUs, and from half the CUs' worth with M >= 1024 (fp8 M=1024,
-    //    K=N=8192: 128 tiles, 88 against 105 for 128-row register-staged tiles);
+    //  * the 256-row kernel once its tiles cover the CUs, and from 5/8 of the CUs' worth with M >= 1024 (int8 M=1024,
+    //    K=8192, N=10240: 160 tiles, 113 against 130 for 128-row ring tiles; at 128 tiles the ring is ahead: fp8
+    //    M=1024, K=N=8192, 89 against 117, int8 K=28672, N=8192, 297 against 353);
     //  * below that the ring kernel: 128-row tiles once they number 5/8 of the CUs (fp8 M=512: 256 tiles, 47 against
     //    62 for 64 x 128), else 64-row tiles (fp8 M=256: 33 against 65 for the register-staged 64 x 64 tiles).
     if (skinny_ok && M <= 16 && K >= 16384) return 16;
     const int64_t tiles = fg::mm_big_tiles(M, N), cus = fg::device_cus();
-    if (tiles >= cus || (M >= 1024 && 2 * tiles >= cus)) return 256;
+    if (tiles >= cus || (M >= 1024 && 8 * tiles >= 5 * cus)) return 256;
     *ring = true;
     const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
     return (M > 64 && 8 * t128 >= 5 * cus) ? 128 : 64;
