@@ -353,7 +353,8 @@ bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const
 }
 
 // Row tile and K splits: 256 x 256 tiles when they alone cover the CUs, 64 x 256 for M <= 64, else 128 x 256, split
-// over K (in 64-column slices, at least 512 columns each) until about one workgroup per CU exists.
+// over K (in 64-column slices, at least 512 columns each) into as many parts as keep the workgroups within one round
+// over the CUs.
 void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kchunk) {
   const int cus = 256;
   const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + kW4BigBN - 1) / kW4BigBN);
@@ -363,7 +364,9 @@ void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kc
   const int64_t tiles = *bm == 256 ? t256 : (*bm == 128 ? t128 : t64);
   int s = split_k;
   if (s <= 0) {
-    s = tiles >= cus ? 1 : (int)((cus + tiles - 1) / tiles);
+    // as many splits as fit in one round of workgroups (gate+up at M = 64 / 128, 112 tiles: 2 splits take 57.5 / 71.3
+    // us, 3 -- a round and a third -- 60.1 / 85.0)
+    s = tiles >= cus ? 1 : (int)(cus / tiles);
     const int max_s = K / 512 > 0 ? K / 512 : 1;
     if (s > max_s) s = max_s;
     if (s > 16) s = 16;
