@@ -138,7 +138,7 @@ constexpr int64_t kMaxDim = (int64_t)1 << 31;
 // tile_n (32, 64, 128; 128 only for 128-row tiles) or mm_ring_bn choosing the width, else the register-staged tiled
 // kernel with square tiles.  Tile 16 selects the skinny kernel (M <= 64, K % 256 == 0, same alignment;
 // register-resident split-K).  Returns the tile (16, 64, 128, 256) and sets *ring when the ring kernel runs; -1 for a
-// configuration the operands do not allow.
+// configuration the operands do not allow, -2 for a tile_m outside 0 / 16 / 64 / 128 / 256.
 int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t lda, const void* b, int64_t ldb,
             const fg_mm_config* cfg, bool* ring) {
   const bool big_ok = fg::mm_big_ok(a, lda, b, ldb, K);
@@ -146,6 +146,7 @@ int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t l
   *ring = false;
   if (cfg && cfg->tile_m) {
     const int t = cfg->tile_m, tn = cfg->tile_n;
+    if (t != 16 && t != 64 && t != 128 && t != 256) return -2;
     if ((t == 256 && !big_ok) || (t == 16 && !skinny_ok)) return -1;
     if (t == 64 || t == 128) {
       if (tn && (!big_ok || (t == 64 && tn != 32 && tn != 64 && tn != 128) || (t == 128 && tn != 128))) return -1;
@@ -468,8 +469,11 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
     if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_int8_gemm: bad bias dtype");
   }
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
+  if (y_dtype == FG_I32 && bias)
+    return fail(FG_EINVAL, "fg_int8_gemm: a bias cannot be added to the raw int32 accumulator (y_dtype FG_I32)");
   bool ring;
   const int tile = mm_tile(M, N, K, true, a, lda, b, ldb, cfg, &ring);
+  if (tile == -2) return fail(FG_EINVAL, "fg_int8_gemm: tile_m must be 0, 16, 64, 128 or 256, got %d", cfg->tile_m);
   if (tile < 0)
     return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
                                  "both 16-byte aligned operands; tile_n (32, 64, 128 for tile_m=64, 128 for "
@@ -510,6 +514,7 @@ int fg_fp8_gemm(const uint8_t* a, int64_t lda, const float* sa, int64_t sa_sm, i
     if (scale_mode == 0) sa_sm = sb_sn = 0;
     bool ring;
     const int tile = mm_tile(M, N, K, false, a, lda, b, ldb, cfg, &ring);
+    if (tile == -2) return fail(FG_EINVAL, "fg_fp8_gemm: tile_m must be 0, 16, 64, 128 or 256, got %d", cfg->tile_m);
     if (tile < 0)
       return fail(FG_EUNSUPPORTED, "fg_fp8_gemm: tile_m=256 needs K %% 128 == 0, tile_m=16 M <= 64 and K %% 256 == 0, "
                                    "both 16-byte aligned operands; tile_n (32, 64, 128 for tile_m=64, 128 for "

@@ -356,7 +356,7 @@ bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const
 // over K (in 64-column slices, at least 512 columns each) into as many parts as keep the workgroups within one round
 // over the CUs.
 void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kchunk) {
-  const int cus = 256;
+  const int cus = device_cus();
   const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + kW4BigBN - 1) / kW4BigBN);
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + kW4BigBN - 1) / kW4BigBN);
   const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + kW4BigBN - 1) / kW4BigBN);

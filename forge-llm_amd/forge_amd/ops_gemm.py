@@ -506,6 +506,8 @@ def int8_gemm(xq: torch.Tensor, sx: torch.Tensor | None, wq: torch.Tensor, sw: t
     if m == 0:
         return y.reshape(*lead, n)
     if out_dtype == torch.int32:
+        if bias is not None:
+            raise ConfigError("int8_gemm: a bias cannot be added to the raw int32 accumulator (out_dtype=torch.int32)")
         sa = sb = None
         sal = sbl = 0
     else:

@@ -127,7 +127,7 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
  * Replaces forge/kernels/triton/gemm_int8.py:95-137 (int8_gemm_triton), called from int8_linear
  * (forge/kernels/ops_gemm.py:483-515).
  *   sa  float [sa_len], sa_len in {1, M};  sb float [sb_len], sb_len in {1, N}
- *   y_dtype  FG_F32 | FG_F16 | FG_BF16, or FG_I32 to store the raw int32 accumulator (scales and bias ignored)
+ *   y_dtype  FG_F32 | FG_F16 | FG_BF16, or FG_I32 to store the raw int32 accumulator (scales ignored; a bias is rejected)
  * ------------------------------------------------------------------------------------------------------------- */
 int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b, int64_t ldb,
                  const float* sb, int64_t sb_len, const void* bias, int bias_dtype, void* y, int64_t ldy, int y_dtype,

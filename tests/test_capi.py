@@ -48,6 +48,23 @@ def test_version_and_error_reporting_without_gpu():
     assert rc == _lib.EINVAL
 
 
+def test_mm_config_and_int32_bias_are_validated_before_launch():
+    """Host-side rejections (the pointers are placeholders that no kernel ever sees)."""
+    L = _lib.lib()
+    dummy = ctypes.c_void_p(256)
+    rc = L.fg_int8_gemm(dummy, 128, None, 0, dummy, 128, None, 0, dummy, _lib.F32, dummy, 64, _lib.I32, 64, 64, 128,
+                        None, None)
+    assert rc == _lib.EINVAL and "bias" in _lib.last_error()
+    for t in (32, 512, 1):
+        cfg = _lib.MMConfig(t, 0)
+        rc = L.fg_int8_gemm(dummy, 128, None, 0, dummy, 128, None, 0, None, 0, dummy, 64, _lib.I32, 64, 64, 128,
+                            ctypes.byref(cfg), None)
+        assert rc == _lib.EINVAL and "tile_m" in _lib.last_error(), t
+        rc = L.fg_fp8_gemm(dummy, 128, dummy, 1, 0, dummy, 128, dummy, 1, 0, 1, 1, 128, None, 0, dummy, 64, _lib.BF16,
+                           64, 64, 128, ctypes.byref(cfg), None)
+        assert rc == _lib.EINVAL and "tile_m" in _lib.last_error(), t
+
+
 @pytest.mark.parametrize("m,n,k,expect_ws", [(1, 4096, 4096, False), (4, 4096, 4096, False), (16, 4096, 4096, True),
                                             (4096, 4096, 4096, False)])
 def test_workspace_query_follows_the_kernel_plan(m, n, k, expect_ws):

@@ -1,0 +1,131 @@
+"""GPU parity of the kernels the automatic per-shape policy picks at the configs' full sizes, where no other test
+forces them: W4A16 (and W8A16) at 33..64 rows over the Llama-3-8B linears (64-row dequantise-to-LDS tiles plus the
+fixed-order split-K reduce), W4A16 at 4 rows over gate+up (skinny MFMA kernel), 256-row prefill tiles with fp16 x,
+and INT8 W8A8 at configs[4]'s (K, N) = (8192, 57344) and (28672, 8192) for M = 1 and 4096.
+
+Bars: W4/W8A16 within max|y - ref| / max|ref| <= 1e-2 of the fp32 oracle plus the reference's compare() rule;
+INT8 int32 accumulators and the fp32 -> bf16 epilogue bit-exact on sampled rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from forge_amd import layouts as L
+from forge_amd import ops_gemm as ops
+from oracle import gemm as og
+from tests._util import assert_close, gen, oracle_packed, to_f32, w4_parts, x_act
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ODT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
+LLAMA = {"qkv": (4096, 6144), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
+
+
+def _rows_oracle(xs: list[torch.Tensor], packed: dict) -> list[np.ndarray]:
+    """One oracle GEMM over the stacked rows of every case (rows are independent), split back per case."""
+    ref = og.w4a16_gemm_ref(np.concatenate([to_f32(x) for x in xs]), packed)
+    out, r0 = [], 0
+    for x in xs:
+        out.append(ref[r0:r0 + x.shape[0]])
+        r0 += x.shape[0]
+    return out
+
+
+@pytest.mark.parametrize("shape", sorted(LLAMA))
+def test_w4_policy_33_to_64_rows_full_size(shape):
+    """M in {33, 48, 64}: the policy runs the prefill kernel with 64-row tiles and K splits (second launch: the
+    split-K reduce).  Forcing impl=prefill picks the same kernel, so both results are equal bit for bit."""
+    k, n = LLAMA[shape]
+    q, s, z = w4_parts(n, k, 128, False, seed=k + n)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    cases = [(33, torch.bfloat16, True), (48, torch.float16, False), (64, torch.bfloat16, False),
+             (64, torch.float16, True)]
+    xs = [x_act(m, k, xdt, seed=m + i) for i, (m, xdt, _) in enumerate(cases)]
+    refs = _rows_oracle(xs, oracle_packed(q, s, z, 128))
+    for (m, xdt, has_b), x, ref in zip(cases, xs, refs):
+        b = (torch.randn(n, generator=gen(m)) * 0.5).to(xdt) if has_b else None
+        bd = None if b is None else b.to(DEV)
+        y = ops.w4a16_linear(x.to(DEV), p, bd)
+        assert ops.last_path("w4a16_linear") == "hip"
+        r = ref if b is None else (ref + to_f32(b)).astype(np.float32)
+        assert_close(y.cpu(), r, ODT[xdt], what=f"w4 policy {shape} m={m}")
+        yf = ops.w4a16_linear(x.to(DEV), p, bd, config={"impl": "prefill"})
+        assert torch.equal(y, yf), f"{shape} m={m}: policy and forced prefill differ"
+
+
+def test_w4_policy_64_rows_symmetric_qkv():
+    k, n = LLAMA["qkv"]
+    q, s, z = w4_parts(n, k, 128, True, seed=3)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(64, k, torch.bfloat16, seed=4)
+    y = ops.w4a16_linear(x.to(DEV), p)
+    assert_close(y.cpu(), og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, 128)), "bfloat16", what="sym m=64")
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_w4_policy_4_rows_gate_up(xdt):
+    """M=4 over gate+up (4096 x 28672): the skinny MFMA kernel (3..4 rows over weights above 4096 x 4096)."""
+    k, n = LLAMA["gate_up"]
+    q, s, z = w4_parts(n, k, 128, False, seed=7)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(4, k, xdt, seed=8)
+    b = (torch.randn(n, generator=gen(9)) * 0.5).to(xdt)
+    y = ops.w4a16_linear(x.to(DEV), p, b.to(DEV))
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, 128), to_f32(b))
+    assert_close(y.cpu(), ref, ODT[xdt], what="gate_up m=4")
+
+
+@pytest.mark.parametrize("m,n,k,gs,xdt,sdt", [
+    (2048, 8192, 1024, 128, torch.float16, torch.float16),   # 256 tiles of 256 x 256: the 256-row kernel, fp16 x
+    (2048, 8192, 512, -1, torch.bfloat16, torch.float32),    # the same with fp32 scales (plain K loop), one group
+])
+def test_w4_prefill_256_row_tiles(m, n, k, gs, xdt, sdt):
+    q, s, z = w4_parts(n, k, gs, False, seed=m + k, scale_dtype=sdt)
+    p = L.pack_w4(q, s, z, gs).to(DEV)
+    x = x_act(m, k, xdt, seed=k)
+    b = (torch.randn(n, generator=gen(k)) * 0.5).to(xdt)
+    y = ops.w4a16_linear(x.to(DEV), p, b.to(DEV), config={"impl": "prefill"})
+    ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs), to_f32(b))
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"prefill 256-row m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("shape", ["qkv", "down"])
+def test_w8a16_policy_64_rows_prefill_kernel(shape):
+    """W8A16 at M = 64 with group 64 (the skinny kernel needs groups of 128): the prefill kernel's 64-row tiles."""
+    k, n = LLAMA[shape]
+    g = gen(k + n)
+    q = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, k // 64, generator=g) * 0.018 + 0.002).half()
+    p = L.pack_w8(q, s, 64).to(DEV)
+    x = x_act(64, k, torch.bfloat16, seed=5)
+    y = ops.w8a16_linear(x.to(DEV), p)
+    ref = og.w8a16_gemm_ref(to_f32(x), og.pack_w8(q.numpy(), s.float().numpy(), 64))
+    assert_close(y.cpu(), ref, "bfloat16", what=f"w8a16 m=64 {shape}")
+    yf = ops.w8a16_linear(x.to(DEV), p, config={"impl": "prefill"})
+    assert torch.equal(y, yf)
+
+
+def _int8_operands(m, n, k, seed):
+    gd = torch.Generator(device=DEV).manual_seed(seed)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=DEV, generator=gd)
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=DEV, generator=gd)
+    sa = torch.rand(m, device=DEV, generator=gd) * 0.01 + 0.001
+    sw = torch.rand(n, device=DEV, generator=gd) * 0.01 + 0.001
+    return a, w, sa, sw
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 8192, 57344), (1, 8192, 57344), (1, 28672, 8192), (64, 8192, 57344)])
+def test_int8_configs4_shapes_exact(m, k, n):
+    """configs[4] shapes the other tests leave out, through the policy: raw int32 accumulator and bf16 epilogue
+    bit-exact against the oracle on sampled rows (all N columns)."""
+    a, w, sa, sw = _int8_operands(m, n, k, seed=m + k + n)
+    acc = ops.int8_gemm(a, None, w, None, out_dtype=torch.int32)
+    y = ops.int8_gemm(a, sa, w, sw, None, out_dtype=torch.bfloat16)
+    rows = sorted({0, m // 3, (2 * m) // 3, m - 1})
+    xq, wq = a[rows].cpu().numpy(), w.cpu().numpy()
+    ref_acc = og.int8_matmul_exact(xq, wq)
+    assert np.array_equal(acc[rows].cpu().numpy(), ref_acc)
+    ref = og.int8_gemm_ref(xq, sa[rows].cpu().numpy(), wq, sw.cpu().numpy(), None, acc=ref_acc)
+    assert torch.equal(y[rows].cpu(), torch.from_numpy(ref).to(torch.bfloat16))
