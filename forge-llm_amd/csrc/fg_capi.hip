@@ -2,9 +2,11 @@
 // Declarations and the reference interface each one replaces: include/forge_mi355x.h.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/forge_mi355x.h"
@@ -288,11 +290,17 @@ size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   return p.ws_bytes;
 }
 
-int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq, const void* scales,
-                  int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
-                  const int32_t* g_idx, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
-                  int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
-                  size_t workspace_bytes, fg_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// fg_w4a16_gemm and fg_w4a16_gemm_noalloc: validation, plan and launch.  `static_ws` marks the library's own scratch
+// buffer as the workspace (a plan that needs more than it holds is rejected rather than served by an allocation).
+int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq, const void* scales,
+              int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+              const int32_t* g_idx, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+              int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
+              size_t workspace_bytes, fg_stream_t stream, bool static_ws) {
   if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
     return fail(FG_EINVAL, "fg_w4a16_gemm: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   if (M == 0) return FG_OK;
@@ -315,6 +323,10 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
   W4Plan p;
   const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, &p);
   if (rc != FG_OK) return rc;
+  if (static_ws && p.ws_bytes > workspace_bytes)
+    return fail(FG_EINVAL, "fg_w4a16_gemm_noalloc: this launch needs %zu bytes of split-K scratch, the library's static "
+                           "buffer holds %zu (FG_W4A16_SCRATCH_BYTES); call fg_w4a16_gemm with a workspace instead",
+                p.ws_bytes, workspace_bytes);
   if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes))
     return fail(FG_EINVAL, "fg_w4a16_gemm: workspace of %zu bytes needed, %zu given", p.ws_bytes,
                 workspace ? workspace_bytes : (size_t)0);
@@ -373,7 +385,63 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
     e = fg::launch_w4_generic(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias,
                               bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, s);
   }
-  return hip_status(e, "fg_w4a16_gemm launch");
+  return hip_status(e, static_ws ? "fg_w4a16_gemm_noalloc launch" : "fg_w4a16_gemm launch");
+}
+
+// Split-K scratch of fg_w4a16_gemm_noalloc: one copy per GPU, placed by the code object loader (no hipMalloc).  The
+// kernels write every element of the partials they later reduce, so nothing in it needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[FG_W4A16_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per device with that device current.  The
+// array's name is a host-side stand-in; only this address may reach a kernel or a copy.
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "fg_w4a16_gemm_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_noalloc: device %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                          "fg_w4a16_gemm_noalloc: hipGetSymbolAddress(scratch)");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq, const void* scales,
+                  int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* perm,
+                  const int32_t* g_idx, const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N,
+                  int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
+                  size_t workspace_bytes, fg_stream_t stream) {
+  return w4a16_run(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias, bias_dtype,
+                   y, ldy, M, N, K, group_size, n_groups, cfg, workspace, workspace_bytes, stream, false);
+}
+
+int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                          const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
+                          const int32_t* perm, const int32_t* g_idx, const void* bias, int bias_dtype, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t n_groups,
+                          const fg_w4_config* cfg, fg_stream_t stream) {
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc != FG_OK) return rc;
+  return w4a16_run(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias, bias_dtype,
+                   y, ldy, M, N, K, group_size, n_groups, cfg, ws, FG_W4A16_SCRATCH_BYTES, stream, true);
 }
 
 int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int scale_dtype, int64_t lds,

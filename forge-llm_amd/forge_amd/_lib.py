@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libforge_mi
 F32, F16, BF16, E4M3, I8, I32 = 0, 1, 2, 3, 4, 5
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float8_e4m3fn: E4M3,
               torch.int8: I8, torch.int32: I32}
+W4A16_SCRATCH_BYTES = 64 << 20  # FG_W4A16_SCRATCH_BYTES
 # status codes
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 # W4A16 impl codes
@@ -59,6 +60,8 @@ P, I64, I32_, INT, SZ, F32_ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, c
 SIGNATURES = {
     "fg_w4a16_gemm": ([P, I64, INT, P, I64, P, INT, I64, P, I64, P, P, P, INT, P, I64, I64, I64, I64, I32_, I32_,
                        ctypes.POINTER(W4Config), P, SZ, P], INT),
+    "fg_w4a16_gemm_noalloc": ([P, I64, INT, P, I64, P, INT, I64, P, I64, P, P, P, INT, P, I64, I64, I64, I64, I32_,
+                               I32_, ctypes.POINTER(W4Config), P], INT),
     "fg_w4a16_workspace_bytes": ([I64, I64, I64, I32_, I32_, I32_, I32_, ctypes.POINTER(W4Config)], SZ),
     "fg_w4_dequant": ([P, I64, P, INT, I64, P, I64, P, P, INT, I64, I64, I64, I32_, I32_, P], INT),
     "fg_w8a16_gemm": ([P, I64, INT, P, I64, P, INT, I64, P, INT, P, I64, I64, I64, I64, I32_, I32_,

@@ -92,6 +92,21 @@ int fg_w4a16_gemm(const void* x, int64_t ldx, int x_dtype, const int32_t* qweigh
                   int64_t K, int32_t group_size, int32_t n_groups, const fg_w4_config* cfg, void* workspace,
                   size_t workspace_bytes, fg_stream_t stream);
 
+/* W4A16 without a caller workspace.  No counterpart in the reference: an entry point for callers that cannot allocate
+ * device memory (code under HIP graph capture in harnesses that forbid hipMalloc, tight serving loops).  Arguments and
+ * results are those of fg_w4a16_gemm minus the workspace: split-K partials go to a static device buffer of
+ * FG_W4A16_SCRATCH_BYTES that the library holds on every GPU it runs on until the process ends.  A launch whose plan
+ * needs more scratch than that returns FG_EINVAL (call fg_w4a16_gemm with a workspace instead).  Nothing is allocated
+ * and nothing in the buffer needs clearing (each launch writes all the partials it reduces).  Calls that overlap on
+ * one GPU (concurrent streams or host threads) share the buffer and race.  The calling thread's current device must be
+ * the device of `stream` and of the tensors. */
+#define FG_W4A16_SCRATCH_BYTES ((size_t)64 << 20)
+int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                          const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
+                          const int32_t* perm, const int32_t* g_idx, const void* bias, int bias_dtype, void* y,
+                          int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t n_groups,
+                          const fg_w4_config* cfg, fg_stream_t stream);
+
 /* Workspace bytes fg_w4a16_gemm needs for this problem and config (0 for single-pass launches).  The alignment and
  * g_idx flags must match the later call: x_aligned = x and ldx allow 16-byte row loads, q_aligned = qweight and ldq
  * allow 16-byte chunk loads, has_g_idx = a per-column g_idx will be passed. */
