@@ -262,26 +262,6 @@ def int8_gemm_ref(xq: np.ndarray, sx: np.ndarray, wq: np.ndarray, sw: np.ndarray
     return y.astype(np.float32)
 
 
-def int8_quant_agreement(x: np.ndarray, q: np.ndarray, s: np.ndarray, q_ref: np.ndarray, s_ref: np.ndarray,
-                         tie_tol: float = 1e-6) -> dict:
-    """Kernel-vs-oracle agreement of a per-token int8 quantisation (``forge/kernels/ref/gemm_int8.py:38-59``):
-    scale distance in ulps, and code mismatches not explained by an exact ``k + 0.5`` tie."""
-    x2 = np.asarray(x, dtype=np.float32)
-    sf, rf = np.asarray(s, np.float32).reshape(-1), np.asarray(s_ref, np.float32).reshape(-1)
-    ulp = np.maximum(np.spacing(np.abs(rf)), np.float32(1e-45))
-    scale_ulp = float((np.abs(sf - rf) / ulp).max()) if rf.size else 0.0
-    diff = np.asarray(q).astype(np.int64).reshape(x2.shape) - np.asarray(q_ref).astype(np.int64).reshape(x2.shape)
-    bad = diff != 0
-    r = x2 / rf.reshape(-1, 1)
-    near_tie = np.abs((r - np.floor(r)) - 0.5) < tie_tol
-    return {
-        "scale_ulp_max": scale_ulp,
-        "code_mismatches": int(bad.sum()),
-        "untied_mismatches": int((bad & ~near_tie).sum()),
-        "max_code_diff": int(np.abs(diff).max()) if diff.size else 0,
-    }
-
-
 # ---------------------------------------------------------------------------------------------------- compare
 SPEC_TOL = {"rel": 2e-3, "abs": 1e-3, "rel_norm": 2e-2}  # forge/kernels/specs/{w4a16_gemm,fp8_gemm,int8_w8a8_gemm}.yaml
 

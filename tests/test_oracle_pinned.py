@@ -251,6 +251,73 @@ def test_fp8_gemm_ref_matches_float64_dequant(gx, gw, m, n, k):
 
 
 # ------------------------------------------------------------------------------------------- INT8
+# ------------------------------------------------------------------------------------------- fused RMSNorm -> fp8
+def _rms64(x, w, eps):
+    """``y = x / sqrt(mean(x^2) + eps) * w`` in float64 (the definition, forge/kernels/ref/gemm_fp8.py:130-150)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    y = x64 / np.sqrt((x64 * x64).mean(axis=-1, keepdims=True) + eps)
+    return y if w is None else y * np.asarray(w, dtype=np.float64)
+
+
+def _rmsnorm_pin_failures(fn) -> list[str]:
+    """Every check that ``fn`` (an rmsnorm_act_quant_fp8_ref candidate) fails; [] for a correct one."""
+    bad = []
+    # closed form on random rows (float32 arithmetic: a few ulps of pairwise-sum and sqrt error)
+    for k, seed in ((1, 1), (7, 2), (64, 3), (1000, 4), (4096, 5)):
+        x = rnd(5, k, seed=seed, scale=3.0).astype(np.float32)
+        w = (np.abs(rnd(k, seed=seed + 10)) + 0.5).astype(np.float32)
+        q, s, y = fn(x, w, 1e-6)
+        y64 = _rms64(x, w, 1e-6)
+        if not np.all(np.abs(y - y64) <= 2e-6 * np.abs(y64) + 1e-30):
+            bad.append(f"closed form k={k}")
+        q2, s2 = og.quantize_fp8_ref(y, "per_token")
+        if not (np.array_equal(q, q2) and np.array_equal(s, s2)):
+            bad.append(f"quantisation of y k={k}")
+    # constant row c: y = c / sqrt(c^2 + eps); eps inside the root, a mean (not a sum) over K
+    x = np.full((1, 16), 2.0, np.float32)
+    _, _, y = fn(x, None, 0.25)
+    if not np.allclose(y, 2.0 / np.sqrt(4.25), rtol=1e-7, atol=0):
+        bad.append("constant row")
+    # the weight multiplies after the normalisation, element by element
+    _, s, y = fn(np.array([[3.0, 4.0]], np.float32), np.array([2.0, 0.5], np.float32), 1.0)
+    if not np.allclose(y, np.array([[6.0, 2.0]]) / np.sqrt(13.5), rtol=1e-7, atol=0):
+        bad.append("weight / eps placement")
+    if not np.isclose(s[0], 6.0 / np.sqrt(13.5) / 448.0, rtol=1e-7):
+        bad.append("scale = amax(y) / 448")
+    # a zero row normalises to zero: scale 1, codes 0
+    q, s, y = fn(np.zeros((2, 8), np.float32), np.ones(8, np.float32), 1e-6)
+    if not (np.all(y == 0) and np.all(s == 1.0) and np.all(q == 0)):
+        bad.append("zero row")
+    return bad
+
+
+def test_rmsnorm_act_quant_fp8_ref_pinned():
+    assert _rmsnorm_pin_failures(og.rmsnorm_act_quant_fp8_ref) == []
+
+
+def test_rmsnorm_pins_catch_planted_mistakes():
+    """eps outside the root, a sum over K instead of the mean, and the weight applied before the norm all fail."""
+    def eps_outside(x, w, eps):
+        xf = np.asarray(x, np.float32)
+        y = (xf / (np.sqrt((xf * xf).mean(-1, keepdims=True)) + np.float32(eps))).astype(np.float32)
+        y = y if w is None else (y * w).astype(np.float32)
+        return (*og.quantize_fp8_ref(y, "per_token"), y)
+
+    def sum_not_mean(x, w, eps):
+        xf = np.asarray(x, np.float32)
+        y = (xf / np.sqrt((xf * xf).sum(-1, keepdims=True) + np.float32(eps))).astype(np.float32)
+        y = y if w is None else (y * w).astype(np.float32)
+        return (*og.quantize_fp8_ref(y, "per_token"), y)
+
+    def weight_first(x, w, eps):
+        xf = np.asarray(x, np.float32) * (1 if w is None else w)
+        y = (xf / np.sqrt((xf * xf).mean(-1, keepdims=True) + np.float32(eps))).astype(np.float32)
+        return (*og.quantize_fp8_ref(y, "per_token"), y)
+
+    for fn in (eps_outside, sum_not_mean, weight_first):
+        assert _rmsnorm_pin_failures(fn), fn.__name__
+
+
 def test_int8_quant_known_answers_and_ieee_scale():
     """tests/test_kernels_gemm_refs.py:205-213 and :351-359."""
     x = rnd(9, 70, scale=2)
