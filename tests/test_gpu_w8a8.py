@@ -130,7 +130,7 @@ def test_fp8_quantiser_edge_cases():
     qn, sn = ops.quantize_act_fp8(xn.to(DEV))
     qnr, snr = og.quantize_fp8_ref(to_f32(xn), "per_token")
     assert np.array_equal(sn.cpu().numpy(), snr)
-    assert np.array_equal(fp8_codes(qn)[1], qnr[1]) and torch.isfinite(qn[1].float()).all()
+    assert np.array_equal(fp8_codes(qn), qnr) and torch.isfinite(qn[1].float()).all()  # NaN code 0x7F / 0xFF too
 
 
 @pytest.mark.parametrize("k", [64, 1000, 4096, 12288])

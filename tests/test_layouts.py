@@ -125,3 +125,68 @@ def test_simple_int4_to_portable_is_bit_identical(n, k, gs, sym):
         assert a.qweight.data_ptr() == simple.data_ptr()  # a view, no copy
     qq, ss, zz = L.unpack_w4(a)
     assert torch.equal(qq, q) and torch.equal(ss, s) and (zz is None or torch.equal(zz, z))
+
+
+def _cdna4_brute_force(q: torch.Tensor, zeros: torch.Tensor | None, gs: int) -> torch.Tensor:
+    """The cdna4_mfma words placed one code at a time from the layout's definition: tile (nt, kt) at words
+    [nt, 256 kt ..]; lane l = 16 j + r owns words 4 l .. 4 l + 3; word s holds channel 16 nt + r, columns
+    128 kt + 32 s + 8 j + t, column t in nibble slot t // 2 (t even) or 4 + t // 2 (t odd); padding columns hold the
+    group's zero-point (8 when symmetric), padding channels 8."""
+    n, k = q.shape
+    nt, kt = -(-n // 16), -(-k // 128)
+    g = -(-k // gs)
+    words = [[0] * (kt * 256) for _ in range(nt)]
+    for tn in range(nt):
+        for tk in range(kt):
+            for j in range(4):
+                for r in range(16):
+                    for s in range(4):
+                        w = 0
+                        for t in range(8):
+                            ch, col = 16 * tn + r, 128 * tk + 32 * s + 8 * j + t
+                            if ch >= n:
+                                code = 8
+                            elif col >= k:
+                                code = 8 if zeros is None else int(zeros[ch, min(col // gs, g - 1)])
+                            else:
+                                code = int(q[ch, col])
+                            slot = t // 2 if t % 2 == 0 else 4 + t // 2
+                            w |= code << (4 * slot)
+                        words[tn][tk * 256 + 4 * (16 * j + r) + s] = w - (1 << 32) if w >= 1 << 31 else w
+    return torch.tensor(words, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("n,k,gs,sym", [(16, 128, 128, False), (21, 200, 64, False), (40, 384, 128, True),
+                                        (5, 96, -1, False)])
+def test_cdna4_layout_matches_its_definition_and_round_trips(n, k, gs, sym):
+    q, s, z = w4_parts(n, k, gs, sym, seed=n + k)
+    p = L.pack_w4(q, s, z, gs, L.CDNA4_W4)
+    assert p.layout.kind == L.KIND_CDNA4 and p.layout_id.startswith("w4.cdna4_mfma_k128n16.v1-")
+    assert p.qweight.shape == (-(-n // 16), -(-k // 128) * 256)
+    assert torch.equal(p.qweight, _cdna4_brute_force(q, z, L.effective_group(gs, k)))
+    # scales and zero-points are stored exactly as in portable_row; codes survive both repack directions
+    a = L.pack_w4(q, s, z, gs)
+    assert torch.equal(p.scales, a.scales) and ((z is None and p.zeros is None) or torch.equal(p.zeros, a.zeros))
+    for x, y in zip(L.unpack_w4(p), (q, s, z)):
+        assert (x is None and y is None) or torch.equal(x, y)
+    assert torch.equal(L.repack(p, L.PORTABLE_W4).qweight, a.qweight)
+    assert torch.equal(L.repack(a, L.CDNA4_W4).qweight, p.qweight)
+    shapes = L.w4_storage_shapes(L.CDNA4_W4, n, k, L.num_groups(k, gs), z is not None)
+    assert shapes["qweight"] == tuple(p.qweight.shape) and shapes["scales"] == tuple(p.scales.shape)
+
+
+def test_cdna4_unpack_pairs_are_mfma_b_operands():
+    """(word >> 4p) & 0x000F000F is the pair of columns (2p, 2p + 1) of the lane's eight k-step columns."""
+    n, k = 16, 128
+    q = (torch.arange(n * k) % 16).to(torch.uint8).reshape(n, k)
+    q = q[torch.randperm(n, generator=torch.Generator().manual_seed(1))]
+    p = L.pack_w4(q, torch.ones(n, 1).half(), None, -1, L.CDNA4_W4)
+    words = p.qweight[0].to(torch.int64) & 0xFFFFFFFF
+    for lane in (0, 17, 38, 63):
+        j, r = lane // 16, lane % 16
+        for s in range(4):
+            w = int(words[4 * lane + s])
+            for pair in range(4):
+                v = (w >> (4 * pair)) & 0x000F000F
+                cols = 32 * s + 8 * j + 2 * pair
+                assert (v & 0xF, v >> 16) == (int(q[r, cols]), int(q[r, cols + 1]))
