@@ -18,7 +18,10 @@ shapes, in TFLOP/s against the dense fp8 / int8 MFMA peaks, on pre-
 ``roofline``: the dominant kernel (the gate+up GEMV, 61 MB per launch) timed with HIP events on its launch stream;
 ``traffic`` (HBM bytes per launch) comes from the FETCH_SIZE / WRITE_SIZE counter passes summarised in
 profiles/w4_gemv_gate_up_pmc.json (made with ``--pmc-workload``), when that file is present.
-``cpu_baseline``: the C oracle (oracle/c/oracle.c, scalar, one thread) on a bounded sample of the same workload.
+``roofline.measured_peak``: a 1 GiB device copy (read + write counted); the W8A8 rows carry hipBLASLt's time on the
+same operands (``vendor``).  Every timed row reports the mean with the median and IQR of the per-call times.
+``cpu_baseline``: the reference's oracle arithmetic in torch on the host CPU (oracle/torch_ref.py, every thread given
+to the process) on configs[0], plus one FP8 and one INT8 GEMM at M=4096.
 
 Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1]``; prints one JSON line.
 ``python bench.py --pmc-workload``: only a 256 MiB device copy (counter calibration) and 64 gate+up GEMV launches,
@@ -70,8 +73,34 @@ def make_layer_weights(torch, layouts, dev, k, n, gen):
     return layouts.PackedW4(qweight, scales, zeros, layouts.PORTABLE_W4, n, k, GROUP)
 
 
-def time_graph(torch, fn, reps: int, warmup: int) -> float:
-    """Capture fn() once as a HIP graph; replay `warmup` times, then `reps` times between HIP events (ms/replay)."""
+class Timing(float):
+    """Mean milliseconds per call (the float value) with the median and inter-quartile range of the per-call
+    times next to it."""
+
+    def __new__(cls, samples_ms: list[float]):
+        xs = sorted(samples_ms)
+        obj = super().__new__(cls, sum(xs) / len(xs))
+        q = lambda f: xs[min(len(xs) - 1, max(0, round(f * (len(xs) - 1))))]  # noqa: E731
+        obj.median, obj.iqr, obj.n = q(0.5), q(0.75) - q(0.25), len(xs)
+        return obj
+
+    def stats(self, scale: float = 1.0, nd: int = 4) -> dict:
+        return {"median": round(self.median * scale, nd), "iqr": round(self.iqr * scale, nd), "samples": self.n}
+
+
+def _timed_calls(torch, call, reps: int) -> Timing:
+    """`reps` calls of `call()`, each between two HIP events on the current stream (the one the work is launched on)."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for i in range(reps):
+        call()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return Timing([evs[i].elapsed_time(evs[i + 1]) for i in range(reps)])
+
+
+def time_graph(torch, fn, reps: int, warmup: int) -> Timing:
+    """Capture fn() once as a HIP graph; replay `warmup` times, then `reps` times, each replay timed with HIP events."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -84,26 +113,14 @@ def time_graph(torch, fn, reps: int, warmup: int) -> float:
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    st.record()
-    for _ in range(reps):
-        g.replay()
-    en.record()
-    torch.cuda.synchronize()
-    return st.elapsed_time(en) / reps
+    return _timed_calls(torch, g.replay, reps)
 
 
-def time_eager(torch, fn, reps: int, warmup: int) -> float:
+def time_eager(torch, fn, reps: int, warmup: int) -> Timing:
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    st.record()
-    for _ in range(reps):
-        fn()
-    en.record()
-    torch.cuda.synchronize()
-    return st.elapsed_time(en) / reps
+    return _timed_calls(torch, fn, reps)
 
 
 def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -> tuple[dict, dict]:
@@ -126,18 +143,29 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
         decode[f"M{m}"] = row
         log(f"decode M={m}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
     prefill = {}
+    dense = {name: torch.randn(n, k, device=dev, generator=gen).bfloat16() for name, (k, n) in SHAPES.items()}
     for m in (512, 2048, 8192):
         row = {}
         for name, (k, n) in SHAPES.items():
-            p = next(p for nm, _, p in ring if nm == name)
+            ws = [p for nm, _, p in ring if nm == name][:4]  # four distinct weights, graph-replayed in turn
             x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
-            fn = lambda x=x, p=p: ops.w4a16_linear(x, p)  # noqa: E731
-            ms = time_eager(torch, fn, max(5, steps // 2), 2)
+
+            def run(x=x, ws=ws):
+                for p in ws:
+                    ops.w4a16_linear(x, p)
+
+            t = time_graph(torch, run, max(5, steps // 2), 2)
+            ms = t / len(ws)
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-            row[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+            # the reference's large-M route after its dequantised copy: hipBLASLt's bf16 GEMM via F.linear
+            vend = time_graph(torch, lambda x=x, w=dense[name]: torch.nn.functional.linear(x, w),
+                              max(5, steps // 2), 2)
+            row[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "median_ms": round(t.median / len(ws), 4), "vendor_bf16_gemm_ms": round(vend, 4)}
             del x
         prefill[f"M{m}"] = row
         log(f"prefill M={m}: " + "  ".join(f"{nm} {v['ms']:.3f} ms {v['tflops']:.0f} TF" for nm, v in row.items()))
+    del dense
     return decode, prefill
 
 
@@ -169,14 +197,18 @@ def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -
     return out
 
 
+RING_BYTES = 800 << 20  # >= 3x the 256 MB Infinity Cache: every weight byte of a replayed ring comes from HBM
+
+
 def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
     """configs[3] fp8 at M in {16, 256} (K = N = 8192) and configs[4] int8 at M in {1, 64} on the three 70B shapes:
     HBM-bound, reported in GB/s of algorithmic bytes (weights N*K + activations M*K + scales + bf16 output) and in
-    TFLOP/s."""
+    TFLOP/s; HIP-graph replays over a ring of distinct weights of at least 800 MB."""
     out = {}
     gen = torch.Generator(device=dev).manual_seed(11)
     k, n = 8192, 8192
-    ring = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.float8_e4m3fn) for _ in range(6)]
+    ring = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.float8_e4m3fn)
+            for _ in range(-(-RING_BYTES // (n * k)))]
     sw = torch.rand(n, device=dev, generator=gen) * 0.01
     for m in (16, 256):
         xq = torch.randn(m, k, device=dev, generator=gen).to(torch.float8_e4m3fn)
@@ -186,14 +218,16 @@ def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
             for w in ring:
                 ops.fp8_linear(xq, w, sw, x_scale=sx, out_dtype=torch.bfloat16)
 
-        ms = time_eager(torch, run, reps, 3) / len(ring)
+        t = time_graph(torch, run, reps, 3)
+        ms = t / len(ring)
         by = n * k + m * k + 4 * (m + n) + 2 * m * n
         out[f"fp8_m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
-                                      "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+                                      "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1),
+                                      "median_us": round(t.median / len(ring) * 1e3, 2)}
         log(f"fp8 M={m} K=N=8192: {ms * 1e3:.1f} us  {out[f'fp8_m{m}_k{k}_n{n}']['GBps']:.0f} GB/s")
     del ring
     for (k8, n8) in ((8192, 10240), (8192, 57344), (28672, 8192)):
-        nring = max(2, min(6, (1536 << 20) // (n8 * k8)))
+        nring = max(2, -(-RING_BYTES // (n8 * k8)))
         ring = [torch.randint(-127, 128, (n8, k8), dtype=torch.int8, device=dev, generator=gen) for _ in range(nring)]
         swi = torch.rand(n8, device=dev, generator=gen) * 0.01
         for m in (1, 64):
@@ -204,17 +238,33 @@ def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
                 for w in ring:
                     ops.int8_linear(xi, w, swi, x_scale=sxi, out_dtype=torch.bfloat16)
 
-            ms = time_eager(torch, run, reps, 3) / len(ring)
+            t = time_graph(torch, run, reps, 3)
+            ms = t / len(ring)
             by = n8 * k8 + m * k8 + 4 * (m + n8) + 2 * m * n8
             key = f"int8_m{m}_k{k8}_n{n8}"
             out[key] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
-                        "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                        "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "median_us": round(t.median / len(ring) * 1e3, 2)}
             log(f"int8 M={m} K={k8} N={n8}: {ms * 1e3:.1f} us  {out[key]['GBps']:.0f} GB/s")
         del ring
     return out
 
 
+def _vendor(torch, fn, reps: int) -> Timing | None:
+    """A vendor-library call timed like ours, or None where this torch build lacks it for these operands."""
+    try:
+        fn()
+        torch.cuda.synchronize()
+    except (RuntimeError, TypeError, NotImplementedError) as e:
+        log(f"vendor call unavailable: {type(e).__name__}: {str(e)[:120]}")
+        return None
+    return time_eager(torch, fn, reps, 2)
+
+
 def bench_w8a8(torch, ops, dev, reps: int) -> dict:
+    """configs[3] FP8 at M=4096 and configs[4] INT8 at M=4096 on pre-quantised operands, against the dense MFMA peaks
+    and against hipBLASLt through torch on the same operands (``torch._scaled_mm`` rowwise, ``torch._int_mm``): the
+    measured denominators next to the datasheet ones."""
     out = {}
     gen = torch.Generator(device=dev).manual_seed(7)
     m, k, n = 4096, 8192, 8192
@@ -223,25 +273,50 @@ def bench_w8a8(torch, ops, dev, reps: int) -> dict:
     xq, sx = ops.quantize_act_fp8(x)
     wq, sw = ops.quantize_weight_fp8(w, "per_channel")
     del w
-    fn = lambda: ops.fp8_linear(xq, wq, sw, x_scale=sx, out_dtype=torch.bfloat16)  # noqa: E731
-    ms = time_eager(torch, fn, reps, 3)
-    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    out["fp8_m4096_k8192_n8192"] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4)}
-    log(f"fp8 M=4096 K=N=8192: {ms:.3f} ms  {tf:.0f} TFLOP/s")
-    del xq, wq, x
+    flops = 2.0 * m * n * k
+    t = time_eager(torch, lambda: ops.fp8_linear(xq, wq, sw, x_scale=sx, out_dtype=torch.bfloat16), reps, 3)
+    tf = flops / (t * 1e-3) / 1e12
+    row = {"ms": round(t, 4), "tflops": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4), **t.stats()}
+    wt = wq.t()
+    vend = _vendor(torch, lambda: torch._scaled_mm(xq, wt, scale_a=sx.reshape(m, 1), scale_b=sw.reshape(1, n),
+                                                   out_dtype=torch.bfloat16), reps)
+    if vend is not None:
+        vtf = flops / (vend * 1e-3) / 1e12
+        row["vendor"] = {"op": "torch._scaled_mm rowwise (hipBLASLt)", "ms": round(vend, 4), "tflops": round(vtf, 1)}
+        row["frac_of_vendor"] = round(tf / vtf, 4)
+    out["fp8_m4096_k8192_n8192"] = row
+    log(f"fp8 M=4096 K=N=8192: {t:.3f} ms  {tf:.0f} TFLOP/s" + (f" (vendor {vend:.3f} ms)" if vend else ""))
+    del xq, wq, x, wt
     for (k8, n8) in ((8192, 10240), (8192, 57344), (28672, 8192)):
         xi = torch.randint(-127, 128, (m, k8), dtype=torch.int8, device=dev, generator=gen)
         wi = torch.randint(-127, 128, (n8, k8), dtype=torch.int8, device=dev, generator=gen)
         sxi = torch.rand(m, device=dev, generator=gen) * 0.01
         swi = torch.rand(n8, device=dev, generator=gen) * 0.01
-        fn = lambda: ops.int8_linear(xi, wi, swi, x_scale=sxi, out_dtype=torch.bfloat16)  # noqa: E731
-        ms = time_eager(torch, fn, reps, 3)
-        tops = 2.0 * m * n8 * k8 / (ms * 1e-3) / 1e12
-        out[f"int8_m4096_k{k8}_n{n8}"] = {"ms": round(ms, 4), "tops": round(tops, 1),
-                                          "frac": round(tops / INT8_PEAK_TOPS, 4)}
-        log(f"int8 M=4096 K={k8} N={n8}: {ms:.3f} ms  {tops:.0f} TOP/s")
-        del xi, wi
+        t = time_eager(torch, lambda: ops.int8_linear(xi, wi, swi, x_scale=sxi, out_dtype=torch.bfloat16), reps, 3)
+        ops_n = 2.0 * m * n8 * k8
+        tops = ops_n / (t * 1e-3) / 1e12
+        row = {"ms": round(t, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), **t.stats()}
+        wti = wi.t()
+        vend = _vendor(torch, lambda: torch._int_mm(xi, wti), reps)
+        if vend is not None:
+            vt = ops_n / (vend * 1e-3) / 1e12
+            row["vendor"] = {"op": "torch._int_mm, int32 out (hipBLASLt)", "ms": round(vend, 4), "tops": round(vt, 1)}
+            row["frac_of_vendor"] = round(tops / vt, 4)
+        out[f"int8_m4096_k{k8}_n{n8}"] = row
+        log(f"int8 M=4096 K={k8} N={n8}: {t:.3f} ms  {tops:.0f} TOP/s" + (f" (vendor {vend:.3f} ms)" if vend else ""))
+        del xi, wi, wti
     return out
+
+
+def measure_copy_bandwidth(torch, dev, nbytes: int = 1 << 30, reps: int = 20) -> dict:
+    """Device-to-device copy of `nbytes` (read + write counted), the reference's measured-bandwidth denominator
+    (forge/kernels/bench.py:450-462)."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).normal_()
+    b = torch.empty_like(a)
+    t = time_eager(torch, lambda: b.copy_(a), reps, 5)
+    del a, b
+    return {"op": "torch copy_ 1 GiB (read + write)", "GBps": round(2.0 * nbytes / (t.median * 1e-3) / 1e9, 1),
+            "median_ms": round(t.median, 4)}
 
 
 def pmc_workload(torch, layouts, ops, dev, gen) -> None:
@@ -275,36 +350,75 @@ def load_traffic() -> dict | None:
     return tr if tr.get("kernel", "").split(" ")[0] == DOM_KERNEL.split("<")[0] else None
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict:
-    """The scalar C oracle (one thread) on one decode layer's four W4A16 linears at M=1, repeated to ~`seconds`."""
-    import numpy as np
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
 
-    from oracle import c_oracle
-    from oracle import w4 as ow
+    return platform.processor() or "unknown"
 
-    rng = np.random.default_rng(0)
-    layer = []
-    for name, (k, n) in SHAPES.items():
-        G = k // GROUP
-        p = {"qweight": rng.integers(-2 ** 31, 2 ** 31 - 1, size=(n, k // 8), dtype=np.int64).astype(np.int32),
-             "scales": (rng.random((G, n)) * 0.018 + 0.002).astype(np.float16).astype(np.float32),
-             "zeros": ow.pack_nibbles_int32(rng.integers(6, 10, size=(G, n // 8, 8), dtype=np.uint8)),
-             "g_idx": None, "n": n, "k": k, "group_size": GROUP}
-        layer.append((p, rng.standard_normal((1, k)).astype(np.float32), w4_bytes(1, k, n)))
-    c_oracle.w4a16_gemm(layer[1][1], layer[1][0])  # load the library
-    done_bytes, reps, t0 = 0, 0, time.perf_counter()
-    while True:
-        for p, x, b in layer:
-            c_oracle.w4a16_gemm(x, p)
-            done_bytes += b
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} pass(es) over one Llama-3-8B layer's 4 W4A16 linears at M=1 "
-                      f"(qkv, o_proj, gate_up, down; {sum(b for _, _, b in layer) / 1e6:.1f} MB per pass), "
-                      f"scalar C oracle oracle/c/oracle.c, {el:.1f} s"}
+
+def _cpu_times(fn, reps: int) -> Timing:
+    fn()  # warm-up
+    out = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        out.append((time.perf_counter() - t0) * 1e3)
+    return Timing(out)
+
+
+def cpu_baseline(reps: int = 7) -> dict:
+    """The reference's oracle arithmetic restated in torch (oracle/torch_ref.py) on the host CPU, on every thread this
+    process is given (OMP_NUM_THREADS, else os.cpu_count()): configs[0] (W4A16 GEMV, M=1, K=N=4096, group 128, the
+    configs' distributions) in GB/s of the same algorithmic bytes as ``value``, one warm-up then the median of
+    `reps`; and one stated repeat each of configs[3] FP8 and configs[4] INT8 at M=4096 (TFLOP/s)."""
+    import torch
+
+    from forge_amd import layouts
+    from oracle import torch_ref as tr
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    k = n = 4096
+    G = k // GROUP
+    qweight = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, generator=g)
+    scales = (torch.rand(G, n, generator=g) * 0.018 + 0.002).half()
+    zeros = layouts.pack_nibbles_int32(torch.randint(6, 10, (G, n), dtype=torch.uint8, generator=g).view(G, n // 8, 8))
+    x = torch.randn(1, k, generator=g).bfloat16()
+    t = _cpu_times(lambda: tr.w4a16_gemm(x, qweight, scales, zeros, GROUP).bfloat16(), reps)
+    by = w4_bytes(1, k, n)
+    out = {"value": round(by / (t.median * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+           "kind": "port",
+           "sample": f"configs[0]: W4A16 M=1 K=N=4096 g128 ({by / 1e6:.2f} MB), torch-CPU restatement of "
+                     f"w4a16_gemm_ref (oracle/torch_ref.py), 1 warm-up + median of {reps}",
+           "median_ms": round(t.median, 3), "iqr_ms": round(t.iqr, 3), "threads": torch.get_num_threads(),
+           "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model()}
+    m = 4096
+    xq = torch.randn(m, 8192, generator=g).to(torch.float8_e4m3fn)
+    wq = (torch.randn(8192, 8192, generator=g) * 0.02).to(torch.float8_e4m3fn)
+    sx, sw = torch.rand(m, generator=g) * 0.01, torch.rand(8192, generator=g) * 0.01
+    t0 = time.perf_counter()
+    tr.fp8_gemm(xq, sx, wq, sw).bfloat16()
+    el = time.perf_counter() - t0
+    out["fp8_m4096_k8192_n8192"] = {"s": round(el, 3), "tflops": round(2.0 * m * 8192 * 8192 / el / 1e12, 4),
+                                    "repeats": 1}
+    del xq, wq
+    xi = torch.randint(-127, 128, (m, 8192), dtype=torch.int8, generator=g)
+    wi = torch.randint(-127, 128, (10240, 8192), dtype=torch.int8, generator=g)
+    si, swi = torch.rand(m, generator=g) * 0.01, torch.rand(10240, generator=g) * 0.01
+    t0 = time.perf_counter()
+    tr.int8_gemm(xi, si, wi, swi).bfloat16()
+    el = time.perf_counter() - t0
+    out["int8_m4096_k8192_n10240"] = {"s": round(el, 3), "tops": round(2.0 * m * 8192 * 10240 / el / 1e12, 4),
+                                      "repeats": 1, "note": "exact int32 through a float64 matmul, as the oracle"}
+    return out
 
 
 def main() -> None:
@@ -351,7 +465,8 @@ def main() -> None:
     timer = time_eager if args.eager else time_graph
     ms = timer(torch, step, args.steps, args.warmup)
     value = step_bytes / (ms * 1e-3) / 1e9
-    log(f"step: {ms:.4f} ms, {value:.1f} GB/s ({value / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    log(f"step: {ms:.4f} ms (median {ms.median:.4f}, IQR {ms.iqr:.4f}), {value:.1f} GB/s "
+        f"({value / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     per_shape = {}
     for name, (k, n) in SHAPES.items():
@@ -361,15 +476,21 @@ def main() -> None:
             for x, p in sel:
                 ops.w4a16_linear(x, p)
 
-        t = timer(torch, run, args.steps, args.warmup) / len(sel)
+        tt = timer(torch, run, args.steps, args.warmup)
+        t = tt / len(sel)
         gbs = w4_bytes(1, k, n) / (t * 1e-3) / 1e9
         per_shape[name] = {"K": k, "N": n, "us": round(t * 1e3, 3), "GBps": round(gbs, 1),
-                           "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                           "frac": round(gbs / HBM_PEAK_GBS, 4), "median_us": round(tt.median / len(sel) * 1e3, 3),
+                           "iqr_us": round(tt.iqr / len(sel) * 1e3, 3)}
         log(f"  {name:8s} K={k:5d} N={n:5d}: {t * 1e3:8.3f} us  {gbs:7.1f} GB/s")
+    copy_bw = measure_copy_bandwidth(torch, dev)
+    log(f"copy bandwidth: {copy_bw['GBps']:.0f} GB/s")
     dom = per_shape["gate_up"]
     tr = load_traffic()
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None if tr is None else tr["traffic_bytes"],
+                "measured_peak": copy_bw["GBps"], "frac_of_measured": round(dom["GBps"] / copy_bw["GBps"], 4),
+                "measured_peak_source": copy_bw["op"],
                 "kernel": f"{DOM_KERNEL} (gate_up K=4096 N=28672, M=1)",
                 "bytes_per_launch": w4_bytes(1, 4096, 28672), "avg_launch_us": dom["us"],
                 "traffic_source": None if tr is None else "profiles/w4_gemv_gate_up_pmc.json"}
@@ -382,7 +503,9 @@ def main() -> None:
                       "M": 1, "group_size": GROUP, "layers": LAYERS,
                       "shapes_KN": {k: list(v) for k, v in SHAPES.items()}, "parallelism": "single GPU",
                       "timing": "eager" if args.eager else "hip graph replay"},
-           "frac_of_peak": round(value / HBM_PEAK_GBS, 4), "per_shape": per_shape, "roofline": roofline}
+           "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+           "frac_of_measured_copy": round(value / copy_bw["GBps"], 4),
+           "step_ms": ms.stats(), "per_shape": per_shape, "roofline": roofline}
     if not args.no_sweep:
         out["w4_decode_sweep"], out["w4_prefill"] = bench_w4_sweep(torch, ops, ring, dev, gen, timer, args.steps,
                                                                    args.warmup)

@@ -420,3 +420,33 @@ def test_a_planted_oracle_mistake_is_caught():
     words = p["qweight"].astype(np.int64) & 0xFFFFFFFF
     wrong = np.stack([(words >> (4 * (7 - j))) & 0xF for j in range(8)], axis=-1).reshape(4, 16)
     assert not np.array_equal(wrong, q) and np.array_equal(ow.unpack_w4(p)[0], q)
+
+
+# ------------------------------------------------------------------------------------------- torch-CPU restatement
+def test_torch_restatement_matches_numpy_oracle():
+    """oracle/torch_ref.py (the CPU baseline's arithmetic) against the pinned numpy oracle."""
+    from oracle import torch_ref as tr
+
+    rng = np.random.default_rng(21)
+    for n, k, gs, sym in ((40, 256, 128, False), (17, 200, 64, True), (8, 96, -1, False)):
+        q = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+        g = ow.num_groups(k, gs)
+        s = (rng.random((n, g)) * 0.018 + 0.002).astype(np.float16).astype(np.float32)
+        z = None if sym else rng.integers(0, 16, size=(n, g), dtype=np.uint8)
+        p = ow.pack_w4(q, s, z, gs)
+        qw, sc = torch.from_numpy(p["qweight"]), torch.from_numpy(p["scales"])
+        zz = None if z is None else torch.from_numpy(p["zeros"])
+        w = tr.dequantize(qw, sc, zz, k, gs).numpy()
+        assert np.array_equal(w, ow.dequantize_parts(q, s, z, gs))
+        x = rnd(5, k, seed=n)
+        np.testing.assert_allclose(tr.w4a16_gemm(torch.from_numpy(x), qw, sc, zz, gs).numpy(), og.w4a16_gemm_ref(x, p),
+                                   rtol=2e-5, atol=2e-5)
+    xq, sx = og.quantize_int8_ref(rnd(9, 300, seed=3))
+    wq, sw = og.quantize_int8_ref(rnd(33, 300, seed=4, scale=0.05), "per_channel")
+    y = tr.int8_gemm(torch.from_numpy(xq), torch.from_numpy(sx), torch.from_numpy(wq), torch.from_numpy(sw))
+    assert np.array_equal(y.numpy(), og.int8_gemm_ref(xq, sx, wq, sw))
+    fq, fsx = og.quantize_fp8_ref(rnd(9, 300, seed=5))
+    fw, fsw = og.quantize_fp8_ref(rnd(33, 300, seed=6, scale=0.05), "per_channel")
+    y = tr.fp8_gemm(torch.from_numpy(fq).view(torch.float8_e4m3fn), torch.from_numpy(fsx),
+                    torch.from_numpy(fw).view(torch.float8_e4m3fn), torch.from_numpy(fsw))
+    np.testing.assert_allclose(y.numpy(), og.fp8_gemm_ref(fq, fsx, fw, fsw), rtol=2e-5, atol=1e-6)
