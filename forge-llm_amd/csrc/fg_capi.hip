@@ -55,6 +55,11 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
                          int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
                          hipStream_t s);
 size_t w4_gemv_lds_bytes(int mt, int K);
+bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int sdt, int64_t lds, int64_t ldz, int M,
+                int64_t N, int64_t K, int gs, int64_t G);
+hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                          int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, hipStream_t s);
 hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
@@ -442,6 +447,39 @@ int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t
   if (rc != FG_OK) return rc;
   return w4a16_run(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, perm, g_idx, bias, bias_dtype,
                    y, ldy, M, N, K, group_size, n_groups, cfg, ws, FG_W4A16_SCRATCH_BYTES, stream, true);
+}
+
+int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                        const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
+                        const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                        int32_t group_size, int32_t n_groups, fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                (long long)K);
+  if (M == 0) return FG_OK;
+  if (x_dtype != FG_BF16 && x_dtype != FG_F16)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_cdna4: x must be bf16 or fp16");
+  if (!is_float_dt(scale_dtype)) return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: bad scale dtype %d", scale_dtype);
+  if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: bad bias dtype %d", bias_dtype);
+  if (!x || !qweight || !scales || !y) return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: null tensor");
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int64_t G = (K + gs - 1) / gs;
+  if (group_size > 0 && group_size % 8 != 0)
+    return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: group_size must be a multiple of 8 or <= 0, got %d", group_size);
+  const int64_t kpad = (K + 127) / 128 * 128;
+  if (ldq < 2 * kpad || lds < N || ldx < K || ldy < N || (zeros && ldz < (N + 7) / 8))
+    return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: leading dimensions too small (ldq counts int32 words per 16-channel "
+                           "tile row: at least 2 * K rounded up to 128)");
+  if (n_groups < G)
+    return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: n_groups=%d does not cover K=%lld with group %d", n_groups,
+                (long long)K, gs);
+  if (!fg::w4_frag_ok(x, ldx, qweight, ldq, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G))
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_cdna4: needs M <= 64, K %% 128 == 0, group %% 128 == 0 (or one group), "
+                                 "16-bit scales, 16-byte aligned x and qweight, ldx %% 8 == 0, ldq %% 4 == 0");
+  return hip_status(fg::launch_w4_frag(x, ldx, x_dtype == FG_BF16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
+                                       bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G,
+                                       static_cast<hipStream_t>(stream)),
+                    "fg_w4a16_gemm_cdna4 launch");
 }
 
 int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int scale_dtype, int64_t lds,

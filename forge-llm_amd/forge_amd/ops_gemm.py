@@ -344,6 +344,24 @@ def _w4_call(x2: torch.Tensor, ops_: _W4Operands, bias: torch.Tensor | None, y: 
         w.num_groups, _cfg_ref(cfg), _lib.ptr(ws), ws_bytes, _lib.stream_of(x2)), "fg_w4a16_gemm")
 
 
+def _cdna4_fits(p: PackedW4, m: int, config: dict[str, Any] | None) -> bool:
+    """Whether the CDNA4-layout kernel serves this call (else the weight's portable copy does)."""
+    impl = forced_impl() or _W4_IMPLS.get((config or {}).get("impl"))
+    return (p.layout.kind == KIND_CDNA4 and 1 <= m <= 64 and p.g_idx is None and p.k % 128 == 0
+            and (p.group_size <= 0 or p.group_size % 128 == 0) and p.scales.dtype in (torch.float16, torch.bfloat16)
+            and impl in (None, "mfma"))
+
+
+def _w4_cdna4_call(x2: torch.Tensor, p: PackedW4, bias: torch.Tensor | None, y: torch.Tensor) -> None:
+    m, k = x2.shape
+    z = p.zeros
+    _check(_lib.lib().fg_w4a16_gemm_cdna4(
+        _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(p.qweight), _ld(p.qweight), _lib.ptr(p.scales),
+        _lib.dtype_code(p.scales.dtype), _ld(p.scales), _lib.ptr(z), 0 if z is None else _ld(z), _lib.ptr(bias),
+        _code_or_zero(bias), _lib.ptr(y), y.stride(0), m, p.n, k, p.group_size, p.num_groups, _lib.stream_of(x2)),
+        "fg_w4a16_gemm_cdna4")
+
+
 def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = None, *,
                  config: dict[str, Any] | None = None, deterministic: bool = True) -> torch.Tensor:
     """``y = x @ dequant(W)^T (+ bias)`` for bf16 / fp16 ``x [..., K]`` on a gfx950 GPU; returns ``x.dtype``.
@@ -351,7 +369,8 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     The C library picks the kernel per shape (``config={"impl": "gemv" | "mfma" | "prefill" | "generic", ...}`` or
     ``FORGE_W4_IMPL`` overrides it): split-K register GEMV for 1-2 rows (and small weights at 3-4), the skinny MFMA
     kernel up to 32 rows, dequantise-to-LDS MFMA tiles beyond, a per-element kernel for irregular act order or
-    unaligned weights.  Every kernel reduces in a fixed order, so results are run-to-run reproducible whatever
+    unaligned weights.  A weight in the ``cdna4_mfma`` layout (``prepare_w4(p, CDNA4_W4)``) runs its own MFMA kernel
+    for 1..64 rows and a portable_row copy beyond.  Every kernel reduces in a fixed order, so results are run-to-run reproducible whatever
     ``deterministic`` says.
     """
     _on_gpu(x, "w4a16_linear")
@@ -362,10 +381,17 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     if packed.qweight.device != x.device:
         raise ConfigError(f"the weight is on {packed.qweight.device}, x on {x.device}")
     x2 = _as_rows(x)
-    y = torch.empty((x2.shape[0], packed.n), dtype=x.dtype, device=x.device)
-    if x2.shape[0]:
+    m = x2.shape[0]
+    y = torch.empty((m, packed.n), dtype=x.dtype, device=x.device)
+    if m:
         b = None if bias is None else bias.contiguous()
-        _w4_call(x2, _w4_operands(packed, _capturing(x2)), b, y, _w4_config(config))
+        if _cdna4_fits(packed, m, config):
+            _w4_cdna4_call(x2, packed, b, y)
+        else:
+            if packed.layout.kind == KIND_CDNA4:
+                _warn_once("cdna4_copy", "a cdna4_mfma W4 weight met a call its kernel does not take (more than 64 rows, "
+                                         "a forced impl, or its shape): a portable_row copy serves it and is kept")
+            _w4_call(x2, _w4_operands(packed, _capturing(x2)), b, y, _w4_config(config))
     _done("w4a16_linear")
     return y.reshape(*x.shape[:-1], packed.n)
 

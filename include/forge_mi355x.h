@@ -113,6 +113,19 @@ int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t
 size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t x_aligned,
                                 int32_t q_aligned, int32_t has_g_idx, const fg_w4_config* cfg);
 
+/* W4A16 on the CDNA4 MFMA-fragment layout w4.cdna4_mfma_k128n16 (forge_amd.layouts.CDNA4_W4), for 1 <= M <= 64.
+ * The reference reserves a "native" executor for fragment-ordered W4 layouts that kernels read without shuffles
+ * (forge/kernels/layouts/layout.py:14-17,158-190, w4.py:18-24) but ships no kernel for it; this is that kernel for
+ * gfx950, over this build's fragment order (v_mfma_f32_16x16x32 B operands; load-time repack in
+ * forge_amd.layouts.repack / ops_gemm.prepare_w4).  Same arguments and results as fg_w4a16_gemm except:
+ *   qweight  int32 [ceil(N/16), ldq]: 16-channel tile rows, 256 words per 128-column tile, ldq >= 2 * K (K % 128 == 0)
+ *   no perm / g_idx (act-order weights are column-sorted first), no workspace (one launch, slices summed in LDS)
+ * Needs group_size % 128 == 0 (or one group), fp16 / bf16 scales, 16-byte aligned x (ldx % 8 == 0) and qweight. */
+int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                        const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
+                        const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                        int32_t group_size, int32_t n_groups, fg_stream_t stream);
+
 /* Dense dequantisation out[n,k] = (q - z) * s computed in fp32 and rounded once to out_dtype (FG_F32|FG_F16|FG_BF16).
  * Replaces forge/kernels/triton/gemm_w4_dequant.py:143-191 (w4_dequant) and PackedW4.dequantize
  * (forge/kernels/layouts/w4.py:137-140 -> dequantize_parts :294-305). */
