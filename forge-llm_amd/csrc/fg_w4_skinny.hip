@@ -86,10 +86,12 @@ __global__ void __launch_bounds__(w4_skinny_max_threads(MB, T)) w4_skinny_kernel
   // per tile: this lane's weight row and the column of its accumulator values (the same channel n0 + 16 t + r16).
   // Offsets are 32-bit from the uniform base pointers (the host checks that every operand spans < 4 GiB).
   const int G = gsteps > 0 ? (K / 128 + gsteps - 1) / gsteps : 1;
-  const __amdgpu_buffer_rsrc_t rq = sk_rsrc(qw, (uint32_t)N * (uint32_t)ldq * 4u);
-  const __amdgpu_buffer_rsrc_t rx = sk_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);
-  const __amdgpu_buffer_rsrc_t rs = sk_rsrc(scales, (uint32_t)G * (uint32_t)lds * 2u);
-  const __amdgpu_buffer_rsrc_t rz = sk_rsrc(zeros, hasz ? (uint32_t)G * (uint32_t)ldz * 4u : 4u);
+  const uint32_t qspan = (uint32_t)N * (uint32_t)ldq * 4u, xspan = (uint32_t)M * (uint32_t)ldx * 2u;
+  const uint32_t sspan = (uint32_t)G * (uint32_t)lds * 2u, zspan = hasz ? (uint32_t)G * (uint32_t)ldz * 4u : 4u;
+  const __amdgpu_buffer_rsrc_t rq = sk_rsrc(qw, qspan);
+  const __amdgpu_buffer_rsrc_t rx = sk_rsrc(x, xspan);
+  const __amdgpu_buffer_rsrc_t rs = sk_rsrc(scales, sspan);
+  const __amdgpu_buffer_rsrc_t rz = sk_rsrc(zeros, zspan);
   uint32_t woff[T], soff[T], zoff[T];
   int ncol[T];
 #pragma unroll
@@ -118,18 +120,19 @@ __global__ void __launch_bounds__(w4_skinny_max_threads(MB, T)) w4_skinny_kernel
     return make_uint4(v[0], v[1], v[2], v[3]);
   };
   auto fetch = [&](int st, Buf& b) __attribute__((always_inline)) {
+    const bool live = st < st1;
     const uint32_t g = gsteps > 0 ? gdiv.div((uint32_t)st) : 0u;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b.x[i][q] = ld16(rx, xoff[i] + (uint32_t)st * 256u + 16u * q);
+      for (int q = 0; q < 4; ++q) b.x[i][q] = ld16(rx, live ? xoff[i] + (uint32_t)st * 256u + 16u * q : xspan);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)((g * lds32 + soff[t]) * 2u), 0, 0);
-      b.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)((g * ldz32 + zoff[t]) * 4u), 0, 0);
+      b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, live ? (int)((g * lds32 + soff[t]) * 2u) : (int)sspan, 0, 0);
+      b.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rz, live ? (int)((g * ldz32 + zoff[t]) * 4u) : (int)zspan, 0, 0);
     }
 #pragma unroll
-    for (int t = 0; t < T; ++t) b.w[t] = ld16(rq, woff[t] + (uint32_t)st * 64u);
+    for (int t = 0; t < T; ++t) b.w[t] = ld16(rq, live ? woff[t] + (uint32_t)st * 64u : qspan);
   };
 
   f32x4_sk_t acc[T][MB];
@@ -174,17 +177,16 @@ __global__ void __launch_bounds__(w4_skinny_max_threads(MB, T)) w4_skinny_kernel
     }
   };
 
-  // Steps past the slice re-read its last step (valid, cached) and are not computed: every path issues the same
-  // loads, so the waits before each compute count only loads that are really older.
+  // Steps past the slice are fetched through offsets past the operands' spans: the same load instructions (so the
+  // waits before each compute count exactly the older loads) that read zeros and move no memory.
   if (st0 < st1) {
-    const int last = st1 - 1;
     fetch(st0, bufa);
-    fetch(min(st0 + 1, last), bufb);
+    fetch(st0 + 1, bufb);
     for (int st = st0; st < st1; st += 2) {
       compute(bufa);
-      fetch(min(st + 2, last), bufa);
+      fetch(st + 2, bufa);
       if (st + 1 < st1) compute(bufb);
-      fetch(min(st + 3, last), bufb);
+      fetch(st + 3, bufb);
     }
   }
 

@@ -68,8 +68,9 @@ __global__ void __launch_bounds__(w8_skinny_max_threads(MB, T)) w8_skinny_kernel
   const int st0 = (int)((int64_t)ks * nsteps / KS), st1 = (int)((int64_t)(ks + 1) * nsteps / KS);
   const int r16 = lane & 15, j = lane >> 4;
 
-  const __amdgpu_buffer_rsrc_t ra = w8sk_rsrc(A, (uint32_t)M * (uint32_t)lda);
-  const __amdgpu_buffer_rsrc_t rb = w8sk_rsrc(B, (uint32_t)N * (uint32_t)ldb);
+  const uint32_t aspan = (uint32_t)M * (uint32_t)lda, bspan = (uint32_t)N * (uint32_t)ldb;
+  const __amdgpu_buffer_rsrc_t ra = w8sk_rsrc(A, aspan);
+  const __amdgpu_buffer_rsrc_t rb = w8sk_rsrc(B, bspan);
   uint32_t boff[T], aoff[MB];
 #pragma unroll
   for (int t = 0; t < T; ++t) boff[t] = (uint32_t)min(n0 + 16 * t + r16, N - 1) * (uint32_t)ldb + 64u * j;
@@ -82,15 +83,16 @@ __global__ void __launch_bounds__(w8_skinny_max_threads(MB, T)) w8_skinny_kernel
   };
   Buf bufa, bufb;
   auto fetch = [&](int st, Buf& f) __attribute__((always_inline)) {
+    const bool live = st < st1;
     const uint32_t so = (uint32_t)st * 256u;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) f.a[i][q] = w8sk_ld16(ra, aoff[i] + so + 16u * q);
+      for (int q = 0; q < 4; ++q) f.a[i][q] = w8sk_ld16(ra, live ? aoff[i] + so + 16u * q : aspan);
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) f.b[t][q] = w8sk_ld16(rb, boff[t] + so + 16u * q);
+      for (int q = 0; q < 4; ++q) f.b[t][q] = w8sk_ld16(rb, live ? boff[t] + so + 16u * q : bspan);
   };
   acc_t acc[T][MB];
 #pragma unroll
@@ -105,17 +107,16 @@ __global__ void __launch_bounds__(w8_skinny_max_threads(MB, T)) w8_skinny_kernel
 #pragma unroll
         for (int i = 0; i < MB; ++i) acc[t][i] = Op::mma(f.a[i], f.b[t], s, acc[t][i]);
   };
-  // Steps past the slice re-read its last step (valid, cached) and are not computed, so every path issues the same
-  // loads and each wait before a compute counts only older loads.
+  // Steps past the slice are fetched through offsets past the operands' spans: the same load instructions (so each
+  // wait before a compute counts exactly the older loads) that read zeros and move no memory.
   if (st0 < st1) {
-    const int last = st1 - 1;
     fetch(st0, bufa);
-    fetch(min(st0 + 1, last), bufb);
+    fetch(st0 + 1, bufb);
     for (int st = st0; st < st1; st += 2) {
       compute(bufa);
-      fetch(min(st + 2, last), bufa);
+      fetch(st + 2, bufa);
       if (st + 1 < st1) compute(bufb);
-      fetch(min(st + 3, last), bufb);
+      fetch(st + 3, bufb);
     }
   }
 

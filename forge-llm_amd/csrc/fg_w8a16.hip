@@ -72,9 +72,11 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
   const int r16 = lane & 15, j = lane >> 4;
   const int G = gsteps > 0 ? (nsteps + gsteps - 1) / gsteps : 1;
 
-  const __amdgpu_buffer_rsrc_t rq = w8a_rsrc(qw, (uint32_t)N * (uint32_t)ldq);
-  const __amdgpu_buffer_rsrc_t rx = w8a_rsrc(x, (uint32_t)M * (uint32_t)ldx * 2u);
-  const __amdgpu_buffer_rsrc_t rs = w8a_rsrc(scales, (uint32_t)G * (uint32_t)lds * 2u);
+  const uint32_t qspan = (uint32_t)N * (uint32_t)ldq, xspan = (uint32_t)M * (uint32_t)ldx * 2u;
+  const uint32_t sspan = (uint32_t)G * (uint32_t)lds * 2u;
+  const __amdgpu_buffer_rsrc_t rq = w8a_rsrc(qw, qspan);
+  const __amdgpu_buffer_rsrc_t rx = w8a_rsrc(x, xspan);
+  const __amdgpu_buffer_rsrc_t rs = w8a_rsrc(scales, sspan);
   uint32_t woff[T], soff[T];
   int ncol[T];
 #pragma unroll
@@ -97,17 +99,19 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
   };
   Buf bufa, bufb;
   auto fetch = [&](int st, Buf& b) __attribute__((always_inline)) {
+    const bool live = st < st1;
     const uint32_t g = gsteps > 0 ? gdiv.div((uint32_t)st) : 0u;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b.x[i][q] = w8a_ld16(rx, xoff[i] + (uint32_t)st * 256u + 16u * q);
+      for (int q = 0; q < 4; ++q) b.x[i][q] = w8a_ld16(rx, live ? xoff[i] + (uint32_t)st * 256u + 16u * q : xspan);
 #pragma unroll
-    for (int t = 0; t < T; ++t) b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)((g * lds32 + soff[t]) * 2u), 0, 0);
+    for (int t = 0; t < T; ++t)
+      b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, live ? (int)((g * lds32 + soff[t]) * 2u) : (int)sspan, 0, 0);
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) b.w[t][h] = w8a_ld16(rq, woff[t] + (uint32_t)st * 128u + 16u * h);
+      for (int h = 0; h < 2; ++h) b.w[t][h] = w8a_ld16(rq, live ? woff[t] + (uint32_t)st * 128u + 16u * h : qspan);
   };
 
   f32x4_w8_t acc[T][MB];
@@ -165,16 +169,15 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
     }
   };
 
-  // Steps past the slice re-read its last step (valid, cached) and are not computed.
+  // Steps past the slice are fetched through offsets past the operands' spans: same loads, no memory moved.
   if (st0 < st1) {
-    const int last = st1 - 1;
     fetch(st0, bufa);
-    fetch(min(st0 + 1, last), bufb);
+    fetch(st0 + 1, bufb);
     for (int st = st0; st < st1; st += 2) {
       compute(bufa);
-      fetch(min(st + 2, last), bufa);
+      fetch(st + 2, bufa);
       if (st + 1 < st1) compute(bufb);
-      fetch(min(st + 3, last), bufb);
+      fetch(st + 3, bufb);
     }
   }
 
