@@ -122,6 +122,10 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
     uint4 w, w2;
     uint32_t s, z;
   };
+  // Vector-memory instructions one fetch_w issues (4-bit: weights, scale, zero word; 8-bit: two weight halves,
+  // scale).  The PF = 2 loop waits with vmcnt(kFetchVmem) for the x rows it issued just before them;
+  // tests/test_isa_waits.py checks in the built code object that this many loads follow the last x load.
+  constexpr int kFetchVmem = 3;
   auto fetch_w = [&](int k0, WRegs& r) __attribute__((always_inline)) {
     const uint32_t c = (uint32_t)((k0 >> 5) + whalf);  // 32-column chunk index
     const int g = (int)(__umulhi(c, gmul) | (c & gsel));
@@ -230,7 +234,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       // Slice kt + 1's x rows have landed (slice kt + 2's three loads may still be in flight) and this wave's LDS
       // stores are done; then the workgroup barrier.  Not __syncthreads(): its release fence waits for every load,
       // the prefetch included.  The memory clobber keeps the compiler from moving LDS accesses across it.
-      asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kFetchVmem) : "memory");
     };
     WRegs ra, rb;
     if (nk > 0) {
@@ -239,7 +243,7 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
       stash_w(smem + BM * ROW, ra);
       fetch_w(kbeg + min(1, nk - 1) * BK, rb);
     }
-    asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kFetchVmem) : "memory");
     for (int kt = 0; kt < nk; kt += 2) {  // nk is even (the host splits K in 128-column multiples)
       body(kt, ra, rb, h0, h1, h1 + BM * ROW);
       body(kt + 1, rb, ra, h1, h0, h0 + BM * ROW);
