@@ -142,6 +142,29 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
             row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         decode[f"M{m}"] = row
         log(f"decode M={m}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
+    # the same weights repacked at load time into the CDNA4 MFMA-fragment layout (a bit-exact permutation), read by
+    # its own kernel at 16 and 64 rows
+    from forge_amd import layouts
+
+    frag = [(nm, layouts.repack(p, layouts.CDNA4_W4)) for nm, _, p in ring]
+    torch.cuda.synchronize()
+    for m in (16, 64):
+        row = {}
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
+        for name, (k, n) in SHAPES.items():
+            sel = [(xs[k], p) for nm, p in frag if nm == name]
+
+            def run(sel=sel):
+                for x, p in sel:
+                    ops.w4a16_linear(x, p)
+
+            t = timer(torch, run, steps, warmup) / len(sel)
+            gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
+            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        decode[f"M{m}_cdna4_layout"] = row
+        log(f"decode M={m} (cdna4 layout): " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s"
+                                                       for nm, v in row.items()))
+    del frag
     prefill = {}
     dense = {name: torch.randn(n, k, device=dev, generator=gen).bfloat16() for name, (k, n) in SHAPES.items()}
     for m in (512, 2048, 8192):

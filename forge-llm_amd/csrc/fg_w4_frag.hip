@@ -199,31 +199,21 @@ bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int 
          G * lds * 2 < k4g && G * ldz * 4 < k4g;
 }
 
-// Launch shape.  MB = ceil(M / 16) m-tiles (1, 2 or 4).  T tiles per wavefront from a cost per CU: the tiles of the
-// most loaded CU (channel blocks are dealt whole, ceil(blocks / CUs) each) times 1 + MB / T for the x rows every
-// wavefront reads from L2 (4 MB KiB of x per step against T KiB of weights).  KS K slices per channel block: the
-// most (powers of two, at most 16 wavefronts per CU, at least two steps per slice) the workgroup size allows.  The
-// register ring holds D = 4 / 3 / 2 steps for 1 / 2 / 4 m-tiles.
+// Launch shape, from a sweep of (T, KS) on the Llama-3-8B shapes at M = 1 / 16 / 64 (graph replays over a 1.2 GB
+// weight ring): MB = ceil(M / 16) m-tiles (1, 2 or 4); T = 1 tile per wavefront up to 4096 channels (o_proj, down:
+// 256 channel blocks, one per CU), 2 up to 8192 (qkv), else 4 (gate+up; 2 for 1-4 rows, where the extra tiles only
+// lengthen each wavefront's chain); KS = 4 K slices (2 with 4 tiles), fewer when a slice would be shorter than two
+// steps.  Measured (us): o_proj M=16 7.0 (T1 KS4) against 7.5-16.7 for the others, qkv M=16 8.5 (T2 KS4), gate+up
+// M=16 21.3 (T4 KS2) against 22.0 (T2 KS1) and 25.1 (T4 KS4), down M=16 17.1 (T1 KS4).
 void w4_frag_plan(int M, int N, int K, int* mb, int* T, int* KS) {
-  const int cus = device_cus();
   const int b = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int nsteps = K / 128;
-  int best_t = 1;
-  double best = 0.0;
-  for (int t = 1; t <= 4; t *= 2) {
-    const int64_t nblk = (N + 16 * t - 1) / (16 * t);
-    const double cost = (double)((nblk + cus - 1) / cus) * t * nsteps * (1.0 + (double)b / t);
-    if (t == 1 || cost < best) {
-      best = cost;
-      best_t = t;
-    }
-  }
-  const int64_t per_cu = ((N + 16 * best_t - 1) / (16 * best_t) + cus - 1) / cus;
-  const int wmax = w4_frag_max_threads(b, best_t) / kWave;
-  int ks = 1;
-  while (2 * ks <= wmax && 2 * ks <= 16 && 4 * ks <= nsteps && per_cu * 2 * ks <= 16) ks *= 2;
+  const int t = N <= 4096 ? 1 : (N <= 8192 || M <= 4 ? 2 : 4);
+  int ks = t == 4 ? 2 : 4;
+  while (ks > 1 && 2 * ks > nsteps) ks /= 2;
+  ks = min(ks, w4_frag_max_threads(b, t) / kWave);
   *mb = b;
-  *T = best_t;
+  *T = t;
   *KS = ks;
 }
 
