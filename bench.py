@@ -47,9 +47,9 @@ INT8_PEAK_TOPS = 5000.0  # dense
 SHAPES = {"qkv": (4096, 6144), "o_proj": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
 LAYERS = 32
 GROUP = 128
-# the launch the C library's policy makes for gate+up at M=1: one row of x, one 16-byte chunk per lane, 16 output
-# channels per wavefront (two K slices of 2048 columns, four channel blocks per workgroup)
-DOM_KERNEL = "w4_gemv_split_kernel<1,1,16,bf16>"
+# the launch the C library's policy makes for gate+up at M=1: one row of x, one 16-byte chunk per lane, 8 output
+# channels per wavefront (two K slices of 2048 columns, eight channel blocks per workgroup)
+DOM_KERNEL = "w4_gemv_split_kernel<1,1,8,bf16>"
 METRIC = "W4A16 GEMV HBM GB/s (% peak) at M=1; W8A8 TFLOPS (% MFMA peak) at M=4096"
 
 

@@ -716,16 +716,18 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 }
 
 // Launch shape of the split-K GEMV: S chunks per lane (1 while K <= 32768, else 2 for one row of x), KS =
-// ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront from the rows per CU (more rows amortise the x
-// registers: 16 rows for wide outputs, 4 for narrow ones; R * MT <= 16), BW channel blocks per workgroup (8 .. 16
-// wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
+// ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront (8 for wide outputs or long K, else 4; R * MT <=
+// 16), BW channel blocks per workgroup (8 .. 16 wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
 bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) {
   const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
   const int s = KC <= 16 * kWave ? 1 : (KC <= 32 * kWave && mt == 1 ? 2 : 0);
   if (s == 0) return false;
   const int ks = (KC + kWave * s - 1) / (kWave * s);
   const int per_cu = N / device_cus();
-  int r = per_cu >= 64 ? 16 : ((per_cu >= 20 || ks >= 4) ? 8 : 4);
+  // 8 rows for wide outputs or long K, else 4 (graph replays over a 1.2 GB ring, M = 1: gate+up 12.2 us with 8 rows in
+  // 448 workgroups of 16 wavefronts against 13.2 with 16 rows in one workgroup per CU; qkv 4.75 against 5.03 with 8
+  // rows): fewer rows per wavefront shorten the arithmetic left once a wavefront's last bytes arrive
+  int r = (per_cu >= 64 || ks >= 4) ? 8 : 4;
   if (mt == 2) r = min(r, 8);
   if (mt == 4) r = 4;
   if (s == 2) r = 4;  // 8 rows x 2 chunks would spill
