@@ -24,8 +24,9 @@ same operands (``vendor``).  Every timed row reports the mean with the median an
 to the process) on configs[0], plus one FP8 and one INT8 GEMM at M=4096.
 
 Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1]``; prints one JSON line.
-``python bench.py --pmc-workload``: only a 256 MiB device copy (counter calibration) and 64 gate+up GEMV launches,
-eager, for ``rocprofv3 --pmc`` passes.
+``python bench.py --pmc-workload [gemv|decode|w8a8]``: only a 256 MiB device copy (counter calibration) and the named
+kernels, eager, for ``rocprofv3 --pmc`` passes (gemv: 64 gate+up GEMV launches; decode: the CDNA4-layout kernel at
+M=16/64 on the four shapes; w8a8: the FP8 / INT8 GEMMs at M=4096).
 """
 from __future__ import annotations
 
@@ -342,24 +343,61 @@ def measure_copy_bandwidth(torch, dev, nbytes: int = 1 << 30, reps: int = 20) ->
             "median_ms": round(t.median, 4)}
 
 
-def pmc_workload(torch, layouts, ops, dev, gen) -> None:
-    """Counter-pass workload: a 256 MiB device-to-device copy (known bytes: calibrates FETCH_SIZE / WRITE_SIZE) three
-    times, then the gate+up GEMV (K=4096, N=28672, M=1) over a ring of 32 weights, twice (64 launches)."""
+def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
+    """Counter-pass workloads (no timing), each after a 256 MiB device-to-device copy run three times (known bytes:
+    calibrates FETCH_SIZE / WRITE_SIZE):
+    gemv   -- the gate+up GEMV (K=4096, N=28672, M=1) over a ring of 32 weights, twice (64 launches);
+    decode -- the CDNA4-layout W4 kernel at M=16 and M=64 on the four Llama-3-8B shapes, over a ring of 6 weights per
+              shape, twice (12 launches per shape and M);
+    w8a8   -- the FP8 GEMM at M=4096, K=N=8192 and the INT8 GEMM at M=4096, K=8192, N=10240, 5 launches each."""
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    k, n = SHAPES["gate_up"]
-    x = torch.randn(1, k, device=dev, generator=gen).bfloat16()
-    ring = [make_layer_weights(torch, layouts, dev, k, n, gen) for _ in range(LAYERS)]
-    torch.cuda.synchronize()
-    for _ in range(2):
-        for p in ring:
-            ops.w4a16_linear(x, p)
-    torch.cuda.synchronize()
-    log("pmc workload done: 3 x 256 MiB copy, 64 gate_up GEMV launches")
+    if which == "gemv":
+        k, n = SHAPES["gate_up"]
+        x = torch.randn(1, k, device=dev, generator=gen).bfloat16()
+        ring = [make_layer_weights(torch, layouts, dev, k, n, gen) for _ in range(LAYERS)]
+        torch.cuda.synchronize()
+        for _ in range(2):
+            for p in ring:
+                ops.w4a16_linear(x, p)
+        torch.cuda.synchronize()
+        log("pmc workload done: 3 x 256 MiB copy, 64 gate_up GEMV launches")
+    elif which == "decode":
+        for name, (k, n) in SHAPES.items():
+            ring = [layouts.repack(make_layer_weights(torch, layouts, dev, k, n, gen), layouts.CDNA4_W4)
+                    for _ in range(6)]
+            for m in (16, 64):
+                x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+                torch.cuda.synchronize()
+                for _ in range(2):
+                    for p in ring:
+                        ops.w4a16_linear(x, p)
+                torch.cuda.synchronize()
+            del ring
+        log("pmc workload done: 3 x 256 MiB copy, CDNA4-layout W4 at M=16/64 x 4 shapes x 12 launches")
+    elif which == "w8a8":
+        m = 4096
+        x = torch.randn(m, 8192, device=dev, generator=gen).bfloat16()
+        xq, sx = ops.quantize_act_fp8(x)
+        wq, sw = ops.quantize_weight_fp8(torch.randn(8192, 8192, device=dev, generator=gen) * 0.02, "per_channel")
+        xi = torch.randint(-127, 128, (m, 8192), dtype=torch.int8, device=dev, generator=gen)
+        wi = torch.randint(-127, 128, (10240, 8192), dtype=torch.int8, device=dev, generator=gen)
+        sxi = torch.rand(m, device=dev, generator=gen) * 0.01
+        swi = torch.rand(10240, device=dev, generator=gen) * 0.01
+        torch.cuda.synchronize()
+        for _ in range(5):
+            ops.fp8_linear(xq, wq, sw, x_scale=sx, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            ops.int8_linear(xi, wi, swi, x_scale=sxi, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        log("pmc workload done: 3 x 256 MiB copy, 5 FP8 + 5 INT8 GEMMs at M=4096")
+    else:
+        raise SystemExit(f"unknown counter workload {which!r}")
 
 
 def load_traffic() -> dict | None:
@@ -453,7 +491,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the W4A16 M=4..64 decode and prefill sweeps")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
-    ap.add_argument("--pmc-workload", action="store_true", help="run only the counter-pass workload (no timing)")
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", default=None, choices=("gemv", "decode", "w8a8"),
+                    help="run only a counter-pass workload (no timing): gemv (default), decode or w8a8")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the hot path is a single-GPU kernel; multi-GPU sharding is "
@@ -470,7 +509,7 @@ def main() -> None:
     log(f"device: {torch.cuda.get_device_name(dev)}")
     gen = torch.Generator(device=dev).manual_seed(1234)
     if args.pmc_workload:
-        pmc_workload(torch, layouts, ops, dev, gen)
+        pmc_workload(torch, layouts, ops, dev, gen, args.pmc_workload)
         return
     ring = []  # (name, x, packed)
     xs = {k: torch.randn(1, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}

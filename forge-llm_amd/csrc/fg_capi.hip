@@ -60,6 +60,14 @@ bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int 
 hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
                           int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
                           int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, hipStream_t s);
+bool w4_ring_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+                const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
+bool w4_ring_preferred(int M, int K);
+size_t w4_ring_workspace_bytes(int M, int N, int K);
+hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                          int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
+                          hipStream_t s);
 hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
@@ -449,10 +457,17 @@ int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t
                    y, ldy, M, N, K, group_size, n_groups, cfg, ws, FG_W4A16_SCRATCH_BYTES, stream, true);
 }
 
+size_t fg_w4a16_cdna4_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size) {
+  (void)group_size;
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0 || N >= kMaxDim || K >= kMaxDim) return 0;
+  return fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+}
+
 int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
                         const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
                         const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        int32_t group_size, int32_t n_groups, fg_stream_t stream) {
+                        int32_t group_size, int32_t n_groups, void* workspace, size_t workspace_bytes,
+                        fg_stream_t stream) {
   if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
     return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                 (long long)K);
@@ -476,6 +491,17 @@ int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* 
   if (!fg::w4_frag_ok(x, ldx, qweight, ldq, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G))
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_cdna4: needs M <= 64, K %% 128 == 0, group %% 128 == 0 (or one group), "
                                  "16-bit scales, 16-byte aligned x and qweight, ldx %% 8 == 0, ldq %% 4 == 0");
+  if (fg::w4_ring_preferred((int)M, (int)K) &&
+      fg::w4_ring_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs, G)) {
+    const size_t need = fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
+      return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: needs a 16-byte aligned workspace of %zu bytes, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    return hip_status(fg::launch_w4_ring(x, ldx, x_dtype == FG_BF16, qweight, ldq, scales, scale_dtype, lds, zeros,
+                                         ldz, bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G,
+                                         workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
+                      "fg_w4a16_gemm_cdna4 launch");
+  }
   return hip_status(fg::launch_w4_frag(x, ldx, x_dtype == FG_BF16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
                                        bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G,
                                        static_cast<hipStream_t>(stream)),

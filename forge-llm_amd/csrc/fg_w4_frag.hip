@@ -38,13 +38,18 @@ __device__ __forceinline__ f32x4_fr_t fr_mfma(uint4 a, uint4 b, f32x4_fr_t c) {
   }
 }
 
+// (a & mask) | magic in one VOP3 (mask in a scalar register, magic in a vector register: the encoding takes no
+// literal, and left to itself the compiler emits a v_and + v_or pair with literals)
+__device__ __forceinline__ uint32_t fr_and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
+  return r;
+}
+
 // one k-step's word -> the lane's eight B values (columns 8 j .. 8 j + 7 of the k-step) as four exact 16-bit pairs
-template <bool XBF16>
-__device__ __forceinline__ uint4 fr_unpack(uint32_t w) {
-  constexpr uint32_t kMagic = XBF16 ? 0x43004300u : 0x64006400u;
-  constexpr uint32_t kMask = 0x000F000Fu;
-  return make_uint4((w & kMask) | kMagic, ((w >> 4) & kMask) | kMagic, ((w >> 8) & kMask) | kMagic,
-                    ((w >> 12) & kMask) | kMagic);
+__device__ __forceinline__ uint4 fr_unpack(uint32_t w, uint32_t mask, uint32_t magic) {
+  return make_uint4(fr_and_or(w, mask, magic), fr_and_or(w >> 4, mask, magic), fr_and_or(w >> 8, mask, magic),
+                    fr_and_or(w >> 12, mask, magic));
 }
 
 constexpr int w4_frag_max_threads(int mb, int t) { return mb * t >= 4 ? 256 : 512; }
@@ -64,7 +69,8 @@ __global__ void __launch_bounds__(w4_frag_max_threads(MB, T)) w4_frag_kernel(
   constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
   constexpr int NV = T * MB * 4;  // accumulator values per lane
   extern __shared__ __align__(16) float red[];  // [waves][NV][64]
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);  // K slice and block: uniform
   const int ks = wave % KS, nb = blockIdx.x * ((int)(blockDim.x / kWave) / KS) + wave / KS;
   const int n0 = nb * 16 * T;
   const int nsteps = K / 128;
@@ -76,6 +82,8 @@ __global__ void __launch_bounds__(w4_frag_max_threads(MB, T)) w4_frag_kernel(
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, sp.x);
   const __amdgpu_buffer_rsrc_t rs = buf_rsrc(scales, sp.s);
   const __amdgpu_buffer_rsrc_t rz = buf_rsrc(zeros, sp.z);
+  const __amdgpu_buffer_rsrc_t rq0 = buf_rsrc(qw, 0u), rx0 = buf_rsrc(x, 0u);  // zero length: every load reads 0
+  const __amdgpu_buffer_rsrc_t rs0 = buf_rsrc(scales, 0u), rz0 = buf_rsrc(zeros, 0u);
   // per tile: the lane's 16 bytes of tile-row nt at step 0, and its channel (tiles past the last re-read the last)
   uint32_t woff[T], soff[T], zoff[T];
   int ncol[T];
@@ -100,23 +108,25 @@ __global__ void __launch_bounds__(w4_frag_max_threads(MB, T)) w4_frag_kernel(
     uint32_t s[T], z[T];
   };
   Buf buf[D];
-  // A step past the slice is fetched through offsets past the operands' spans: the same load instructions (so the
-  // waits before each compute count exactly the older loads) that read zeros and move no memory.
+  // A step past the slice is fetched through zero-length buffer resources: the same load instructions (so the waits
+  // before each compute count exactly the older loads) that read zeros and move no memory.  The step and group parts
+  // of each offset are wavefront-uniform (scalar soffset), the lane parts fixed (voffset), so a fetch costs no VALU.
   auto fetch = [&](int st, Buf& b) __attribute__((always_inline)) {
     const bool live = st < st1;
     const uint32_t g = gsteps > 0 ? gdiv.div((uint32_t)st) : 0u;
+    const __amdgpu_buffer_rsrc_t x_ = live ? rx : rx0, q_ = live ? rq : rq0;
+    const __amdgpu_buffer_rsrc_t s_ = live ? rs : rs0, z_ = live ? rz : rz0;
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)  // all in the per-lane offset: the range check sees only that part
-        b.x[i][s] = buf_ld16(rx, live ? xoff[i] + (uint32_t)st * 256u + 64u * (uint32_t)s : sp.x, 0u);
+      for (int s = 0; s < 4; ++s) b.x[i][s] = buf_ld16(x_, xoff[i] + 64u * (uint32_t)s, (uint32_t)st * 256u);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs, live ? (int)(g * lds2 + soff[t]) : (int)sp.s, 0, 0);
-      b.z[t] = __builtin_amdgcn_raw_buffer_load_b32(rz, live ? (int)(g * ldz4 + zoff[t]) : (int)sp.z, 0, 0);
+      b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(s_, (int)soff[t], (int)(g * lds2), 0);
+      b.z[t] = __builtin_amdgcn_raw_buffer_load_b32(z_, (int)zoff[t], (int)(g * ldz4), 0);
     }
 #pragma unroll
-    for (int t = 0; t < T; ++t) b.w[t] = buf_ld16_nt(rq, live ? woff[t] + (uint32_t)st * 1024u : sp.q, 0u);
+    for (int t = 0; t < T; ++t) b.w[t] = buf_ld16_nt(q_, woff[t], (uint32_t)st * 1024u);
   };
 
   f32x4_fr_t acc[T][MB];
@@ -126,15 +136,17 @@ __global__ void __launch_bounds__(w4_frag_max_threads(MB, T)) w4_frag_kernel(
     for (int i = 0; i < MB; ++i) acc[t][i] = f32x4_fr_t{0.f, 0.f, 0.f, 0.f};
 
   const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
+  const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  const uint32_t magic = XBF16 ? 0x43004300u : 0x64006400u;
   auto compute = [&](const Buf& b) __attribute__((always_inline)) {
     uint4 bw[T][4];
     float sc[T], zb[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      bw[t][0] = fr_unpack<XBF16>(b.w[t].x);
-      bw[t][1] = fr_unpack<XBF16>(b.w[t].y);
-      bw[t][2] = fr_unpack<XBF16>(b.w[t].z);
-      bw[t][3] = fr_unpack<XBF16>(b.w[t].w);
+      bw[t][0] = fr_unpack(b.w[t].x, mask, magic);
+      bw[t][1] = fr_unpack(b.w[t].y, mask, magic);
+      bw[t][2] = fr_unpack(b.w[t].z, mask, magic);
+      bw[t][3] = fr_unpack(b.w[t].w, mask, magic);
       sc[t] = SBF16 ? bf16_bits_to_f32(b.s[t]) : f16_bits_to_f32((uint16_t)b.s[t]);
       zb[t] = kB + (hasz ? (float)nibble(b.z[t], ncol[t] & 7) : 8.f);
     }

@@ -1,0 +1,396 @@
+// W4A16 for 1..64 rows of x on the CDNA4 MFMA-fragment weight layout (w4.cdna4_mfma_k128n16), with every operand of a
+// 128-column K step brought into an S-stage LDS ring by direct-to-LDS buffer loads:
+//   y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+bias),  v_mfma_f32_16x16x32_{bf16,f16}.
+//
+// A workgroup of BW wavefronts owns BW * T 16-channel tiles and one K split.  Per step it loads, straight into LDS
+// (no registers, no VALU):
+//   x      the MB * 16 rows x 128 columns of the step, 256 bytes per row, 16-byte unit u of row r stored at
+//          u ^ (r % 16) (the 16 rows of one A-fragment read fall on 16 distinct bank groups); shared by all BW * T
+//          tiles, so x crosses the L2 once per workgroup and step instead of once per wavefront;
+//   W      each tile's 1 KiB for the step, lane l's 16 bytes at l * 16 (the B operand of the four k-steps, in the
+//          order the layout stores them);
+//   s, z   the scales and zero words of the wavefront's channels for the step's group.
+// Each wavefront issues the same NI = 4 MB / BW + T + 2 loads per step, and no other vector-memory load in the loop,
+// so `s_waitcnt vmcnt((S - 2) * NI)` before the step's barrier is exactly "this step has landed" (the loads of the next
+// S - 2 steps stay in flight).  Steps past the split go through a zero-length buffer resource: the same instructions
+// (so the count holds), reading 0 and moving no memory.  Rows of x past M and tiles past N read out of range (0).
+//
+// Arithmetic, as w4_frag_kernel: B = magic | nibble pair ((word >> 4 p) & 0x000F000F | 0x4300 4300 for bf16, 0x6400
+// 6400 for fp16: the exact values 128 + q / 1024 + q), one v_and_or_b32 per pair (plus a shift for p > 0); x row sums
+// from MFMAs against all-ones; per step acc += s * (acc_step - (B + z) * xsum).
+//
+// K splits (KS > 1): each split writes its fp32 partial to the caller's workspace [KS, M, N] and w4_ring_reduce_kernel
+// sums them in split order (bit-reproducible), adds the bias and rounds, eight outputs per thread.  (Letting the last
+// split of a group reduce instead needs a device-scope release per workgroup, an L2 writeback that measured 60-100x
+// slower than the second launch.)
+//
+// Requirements (w4_ring_ok): M <= 64, N % 16 == 0, K % 128 == 0, group size % 128 == 0 or one group, 16-bit scales
+// with lds even and 4-byte aligned scales / zeros, 16-byte aligned x with ldx % 8 == 0, 16-byte aligned qweight with
+// ldq % 4 == 0, every operand spanning < 2 GiB.
+#include "fg_device.h"
+
+namespace fg {
+
+typedef __bf16 bf16x8_rg_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_rg_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_rg_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <bool XBF16>
+__device__ __forceinline__ f32x4_rg_t rg_mfma(uint4 a, uint4 b, f32x4_rg_t c) {
+  if constexpr (XBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_rg_t, a),
+                                                   __builtin_bit_cast(bf16x8_rg_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_rg_t, a),
+                                                  __builtin_bit_cast(f16x8_rg_t, b), c, 0, 0, 0);
+  }
+}
+
+// (a & mask) | magic in one VOP3 (mask in a scalar register, magic in a vector register: the encoding takes no
+// literal, and left to itself the compiler emits a v_and + v_or pair with literals)
+__device__ __forceinline__ uint32_t rg_and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
+  return r;
+}
+
+// one k-step's word -> the lane's eight B values as four exact 16-bit pairs
+__device__ __forceinline__ uint4 rg_unpack(uint32_t w, uint32_t mask, uint32_t magic) {
+  return make_uint4(rg_and_or(w, mask, magic), rg_and_or(w >> 4, mask, magic), rg_and_or(w >> 8, mask, magic),
+                    rg_and_or(w >> 12, mask, magic));
+}
+
+constexpr int kRingBW = 4;  // wavefronts per workgroup
+
+template <int MB, int T, int BW>
+struct RingShape {
+  static_assert((4 * MB) % BW == 0, "the x rows of a step split evenly over the wavefronts");
+  static constexpr int X = MB * 16 * 256;     // x rows of one step
+  static constexpr int W = BW * T * 1024;     // weight tiles of one step
+  static constexpr int SZ = BW * 512;         // per wavefront: 256 bytes of scales, 256 of zero words
+  static constexpr int STAGE = X + W + SZ;
+  static constexpr int XI = 4 * MB / BW;      // x loads (1 KiB = 4 rows each) per wavefront and step
+  static constexpr int NI = XI + T + 2;       // loads per wavefront and step
+};
+
+struct RingArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const int32_t* qw;
+  int64_t ldq;  // int32 words per 16-channel tile row
+  const uint16_t* scales;
+  int64_t lds;
+  const int32_t* zeros;
+  int64_t ldz;
+  const void* bias;
+  float* part;  // KS > 1: fp32 partials [KS, M, N]
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K, gsteps, KS, ngrp, hasz, bdt;
+  uint32_t qbytes, xbytes, sbytes, zbytes;
+};
+
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+__global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
+  using Sh = RingShape<MB, T, BW>;
+  static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
+  constexpr float kB = XBF16 ? 128.f : 1024.f;
+  constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int grp = blockIdx.x % a.ngrp, ks = blockIdx.x / a.ngrp;
+  const int nsteps = a.K / 128;
+  const int st0 = (int)((int64_t)ks * nsteps / a.KS), ns = (int)((int64_t)(ks + 1) * nsteps / a.KS) - st0;
+  const int NT = a.N / 16;
+  const int tile0 = (grp * BW + wave) * T;  // first tile of this wavefront
+  const int r16 = lane & 15, j = lane >> 4;
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, a.xbytes), rq = buf_rsrc(a.qw, a.qbytes);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.scales, a.sbytes), rz = buf_rsrc(a.zeros, a.zbytes);
+  const __amdgpu_buffer_rsrc_t rx0 = buf_rsrc(a.x, 0u), rq0 = buf_rsrc(a.qw, 0u);
+  const __amdgpu_buffer_rsrc_t rs0 = buf_rsrc(a.scales, 0u), rz0 = buf_rsrc(a.zeros, 0u);
+
+  // per-lane load offsets (step 0); rows past M and tiles past N point past their operand
+  uint32_t xv[Sh::XI];
+#pragma unroll
+  for (int q = 0; q < Sh::XI; ++q) {
+    const int row = (wave * Sh::XI + q) * 4 + (lane >> 4);
+    const int u = (lane & 15) ^ (row & 15);
+    xv[q] = row < a.M ? (uint32_t)row * (uint32_t)a.ldx * 2u + 16u * (uint32_t)u : a.xbytes;
+  }
+  uint32_t wv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    wv[t] = tile0 + t < NT ? (uint32_t)(tile0 + t) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)lane : a.qbytes;
+  // scales: lane i < 8 T loads the channel pair 2i, 2i + 1 of the wavefront's tiles; zero words: lane i < 2 T loads
+  // word i (eight channels each)
+  const bool sl = lane < 8 * T && tile0 + lane / 8 < NT, zl = lane < 2 * T && tile0 + lane / 2 < NT;
+  const uint32_t sv = (uint32_t)tile0 * 32u + 4u * (uint32_t)lane, zv = (uint32_t)tile0 * 8u + 4u * (uint32_t)lane;
+  const FastDiv gdiv((uint32_t)max(a.gsteps, 1));
+  const uint32_t lds2 = (uint32_t)a.lds * 2u, ldz4 = (uint32_t)a.ldz * 4u;
+
+  // stage i of the split into the ring slot at stg (i >= ns: zero-length resources, nothing moves)
+  auto issue = [&](int i, uint8_t* stg) __attribute__((always_inline)) {
+    const bool live = i < ns;
+    const int st = st0 + (live ? i : 0);
+    const uint32_t g = a.gsteps > 0 ? gdiv.div((uint32_t)st) : 0u;
+    const __amdgpu_buffer_rsrc_t x_ = live ? rx : rx0, q_ = live ? rq : rq0;
+    const __amdgpu_buffer_rsrc_t s_ = live ? rs : rs0, z_ = live ? rz : rz0;
+#pragma unroll
+    for (int q = 0; q < Sh::XI; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_, (lds_void_t*)(stg + (wave * Sh::XI + q) * 1024), 16, (int)xv[q],
+                                               st * 256, 0, 0);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q_, (lds_void_t*)(stg + Sh::X + (wave * T + t) * 1024), 16,
+                                               (int)wv[t], st * 1024, 0, 2);
+    // the group row goes into the per-lane offset (past-the-end lanes must stay past the end)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * 512), 4,
+                                             sl ? (int)(g * lds2 + sv) : (int)a.sbytes, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(z_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * 512 + 256), 4,
+                                             zl ? (int)(g * ldz4 + zv) : (int)a.zbytes, 0, 0, 0);
+  };
+
+  f32x4_rg_t acc[T][MB];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[t][i] = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
+  const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  const uint32_t magic = XBF16 ? 0x43004300u : 0x64006400u;
+  const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
+
+  auto compute = [&](const uint8_t* __restrict__ stg) __attribute__((always_inline)) {
+    const uint8_t* sw = stg + Sh::X;
+    const uint8_t* ssz = stg + Sh::X + Sh::W + wave * 512;
+    uint4 raw[T];
+    float sc[T], zb[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      raw[t] = *reinterpret_cast<const uint4*>(sw + (wave * T + t) * 1024 + lane * 16);
+      const uint16_t sb = reinterpret_cast<const uint16_t*>(ssz)[t * 16 + r16];
+      sc[t] = SBF16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
+      const uint32_t zw = reinterpret_cast<const uint32_t*>(ssz + 256)[t * 2 + (r16 >> 3)];
+      zb[t] = kB + (a.hasz ? (float)nibble(zw, r16 & 7) : 8.f);
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      uint4 af[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        af[s] = *reinterpret_cast<const uint4*>(stg + (16 * i + r16) * 256 + (((4 * s + j) ^ r16) * 16));
+      f32x4_rg_t xs = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xs = rg_mfma<XBF16>(af[s], ones, xs);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint32_t wq[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
+        f32x4_rg_t as = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) as = rg_mfma<XBF16>(af[s], rg_unpack(wq[s], mask, magic), as);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[t][i][e] = __builtin_fmaf(sc[t], __builtin_fmaf(-zb[t], xs[e], as[e]), acc[t][i][e]);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p) issue(p, smem + p * Sh::STAGE);
+  // The slot being read and the slot being loaded reach the body as __restrict__ pointers, so the compiler does not
+  // wait for the loads in flight before the LDS reads.
+  auto body = [&](int i, const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt) __attribute__((always_inline)) {
+    issue(i + S - 1, nxt);  // the slot of step i - 1: every wavefront has read it (last barrier)
+    __builtin_amdgcn_sched_barrier(0);
+    compute(cur);
+  };
+  for (int i = 0; i < ns; ++i) {
+    // this step's loads have landed for every wavefront, and every wavefront is done with step i - 1's slot
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * Sh::NI) : "memory");
+    body(i, smem + (i % S) * Sh::STAGE, smem + ((i + S - 1) % S) * Sh::STAGE);
+  }
+
+  // KS == 1: y (+ bias); KS > 1: this split's fp32 partial
+  float* part = a.part + (int64_t)ks * a.M * a.N;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * i + 4 * j + e, n = (tile0 + t) * 16 + r16;
+        if (m < a.M && tile0 + t < NT) {
+          float v = acc[t][i][e];
+          if (a.KS > 1) {
+            part[(int64_t)m * a.N + n] = v;
+          } else {
+            if (a.bias) v += load_f(a.bias, a.bdt, n);
+            a.y[(int64_t)m * a.ldy + n] = XBF16 ? f32_to_bf16_bits_hw(v) : f32_to_f16_bits(v);
+          }
+        }
+      }
+}
+
+// y[m, n .. n + 7] = sum over the KS partials in split order (+ bias), one thread per 8 outputs (N % 16 == 0)
+template <bool XBF16>
+__global__ void __launch_bounds__(256) w4_ring_reduce_kernel(const float* __restrict__ part, int KS, int M, int N,
+                                                             const void* __restrict__ bias, int bdt,
+                                                             uint16_t* __restrict__ y, int64_t ldy, int vec_store) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 8 outputs
+  const int n8 = N / 8;
+  if (idx >= (int64_t)M * n8) return;
+  const int m = (int)(idx / n8), n = (int)(idx - (int64_t)m * n8) * 8;
+  const int64_t MN = (int64_t)M * N;
+  f32x4_rg_t a = f32x4_rg_t{0.f, 0.f, 0.f, 0.f}, b = a;
+  const f32x4_rg_t* p = reinterpret_cast<const f32x4_rg_t*>(part + (int64_t)m * N + n);
+  for (int k = 0; k < KS; ++k) {
+    a += p[0];
+    b += p[1];
+    p += MN / 4;
+  }
+  float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  uint16_t h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (bias) v[e] += load_f(bias, bdt, n + e);
+    h[e] = XBF16 ? f32_to_bf16_bits_hw(v[e]) : f32_to_f16_bits(v[e]);
+  }
+  uint16_t* yr = y + (int64_t)m * ldy + n;
+  if (vec_store) {
+    *reinterpret_cast<uint4*>(yr) = make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                                               h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yr[e] = h[e];
+  }
+}
+
+bool w4_ring_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+                const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G) {
+  const int64_t k2g = 1LL << 31;  // offsets past a span plus a step offset stay below 2^32
+  return M > 0 && M <= 64 && sdt != FG_F32 && N % 16 == 0 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) &&
+         (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && ldq >= 2 * K &&
+         (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
+         (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && (reinterpret_cast<uintptr_t>(zeros) % 4) == 0 &&
+         (N / 16) * ldq * 4 < k2g && (int64_t)M * ldx * 2 < k2g && G * lds * 2 < k2g && G * ldz * 4 < k2g;
+}
+
+// Launch shape, from a sweep of (BW, T, KS) against the register-ring kernel (w4_frag_kernel) on the Llama-3-8B
+// shapes at M = 1 / 16 / 32 / 64 (graph replays over a 1.2 GB weight ring): BW = 4 wavefronts; T = 2 tiles per
+// wavefront for 33..64 rows over at least 1024 tiles (gate+up: 37.9 us against 43.2 with one), else 1; KS = 1 when the
+// channel groups fill three quarters of the CUs, else the smallest power of two that fills them, doubled while a split
+// is longer than 16 steps over K >= 8192 (down: 8 splits of 14 steps, 26.0 us at M = 64 against 30.7 with 4).
+// Measured (us, this kernel + reduce / w4_frag_kernel): M = 64 qkv 18.4 / 21.2, o_proj 14.7 / 18.8, gate+up 37.9 /
+// 44.0, down 26.0 / 54.7; M = 32 down 18.7 / 29.9; M = 16 down 15.9 / 17.0.  Below that the register ring is as fast
+// or faster (w4_ring_preferred).
+struct RingPlan {
+  int mb, T, KS, ngrp;
+};
+
+static RingPlan w4_ring_plan(int M, int N, int K) {
+  RingPlan p;
+  p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int NT = N / 16, nsteps = K / 128, cus = device_cus();
+  p.T = p.mb == 4 && NT >= 1024 ? 2 : 1;
+  p.ngrp = (NT + kRingBW * p.T - 1) / (kRingBW * p.T);
+  int ks = 1;
+  if (4 * p.ngrp < 3 * cus)
+    while (p.ngrp * ks < cus && 2 * ks <= nsteps) ks *= 2;
+  if (nsteps >= 64)
+    while (nsteps / ks > 16 && p.ngrp * ks < 4 * cus && 2 * ks <= nsteps) ks *= 2;
+  p.KS = ks;
+  return p;
+}
+
+bool w4_ring_preferred(int M, int K) { return M > 32 || (M > 8 && K >= 8192); }
+
+size_t w4_ring_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || M > 64 || N % 16 != 0 || K % 128 != 0 || !w4_ring_preferred(M, K)) return 0;
+  const RingPlan p = w4_ring_plan(M, N, K);
+  return p.KS == 1 ? 0 : (size_t)p.KS * M * N * sizeof(float);
+}
+
+static hipError_t launch_ring_reduce(bool xbf16, const float* part, int KS, int M, int N, const void* bias, int bdt,
+                                     void* y, int64_t ldy, hipStream_t s) {
+  const int64_t groups = (int64_t)M * (N / 8);
+  const int vec = (reinterpret_cast<uintptr_t>(y) % 16) == 0 && (ldy % 8) == 0;
+  const dim3 grid((unsigned)((groups + 255) / 256));
+  if (xbf16) {
+    hipLaunchKernelGGL(w4_ring_reduce_kernel<true>, grid, dim3(256), 0, s, part, KS, M, N, bias, bdt,
+                       static_cast<uint16_t*>(y), ldy, vec);
+  } else {
+    hipLaunchKernelGGL(w4_ring_reduce_kernel<false>, grid, dim3(256), 0, s, part, KS, M, N, bias, bdt,
+                       static_cast<uint16_t*>(y), ldy, vec);
+  }
+  return hipGetLastError();
+}
+
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
+  using Sh = RingShape<MB, T, BW>;
+  const size_t shm = (size_t)S * Sh::STAGE;
+  auto kern = w4_ring_kernel<MB, T, BW, S, XBF16, SBF16>;
+  if (shm > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(a.ngrp * a.KS), dim3(BW * kWave), shm, s, a);
+  return hipGetLastError();
+}
+
+template <bool XBF16, bool SBF16>
+static hipError_t launch_ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
+  if (p.mb == 1) return launch_ring_t<1, 1, kRingBW, 4, XBF16, SBF16>(a, s);
+  if (p.mb == 2) return launch_ring_t<2, 1, kRingBW, 3, XBF16, SBF16>(a, s);
+  return p.T == 2 ? launch_ring_t<4, 2, kRingBW, 3, XBF16, SBF16>(a, s) : launch_ring_t<4, 1, kRingBW, 3, XBF16, SBF16>(a, s);
+}
+
+hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                          int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
+                          hipStream_t s) {
+  const RingPlan p = w4_ring_plan(M, N, K);
+  RingArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.qw = qw;
+  a.ldq = ldq;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.lds = lds;
+  a.hasz = zeros != nullptr;
+  a.zeros = zeros ? zeros : qw;  // symmetric: never read (zero-length resource below)
+  a.ldz = zeros ? ldz : 0;
+  a.bias = bias;
+  a.bdt = bdt;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.gsteps = single_group ? 0 : gs / 128;
+  a.KS = p.KS;
+  a.ngrp = p.ngrp;
+  a.qbytes = (uint32_t)((int64_t)(N / 16) * ldq * 4);
+  a.xbytes = (uint32_t)((int64_t)M * ldx * 2);
+  a.sbytes = (uint32_t)((int64_t)G * lds * 2);
+  a.zbytes = zeros ? (uint32_t)((int64_t)G * ldz * 4) : 0u;
+  a.part = static_cast<float*>(ws);
+  if (p.KS > 1 && (ws == nullptr || ws_bytes < (size_t)p.KS * M * N * sizeof(float) ||
+                   reinterpret_cast<uintptr_t>(ws) % 16 != 0))
+    return hipErrorInvalidValue;
+  const bool sbf = sdt == FG_BF16;
+  hipError_t e;
+  if (xbf16) {
+    e = sbf ? launch_ring_x<true, true>(p, a, s) : launch_ring_x<true, false>(p, a, s);
+  } else {
+    e = sbf ? launch_ring_x<false, true>(p, a, s) : launch_ring_x<false, false>(p, a, s);
+  }
+  if (e != hipSuccess || p.KS == 1) return e;
+  return launch_ring_reduce(xbf16, a.part, p.KS, M, N, bias, bdt, y, ldy, s);
+}
+
+}  // namespace fg

@@ -355,11 +355,14 @@ def _cdna4_fits(p: PackedW4, m: int, config: dict[str, Any] | None) -> bool:
 def _w4_cdna4_call(x2: torch.Tensor, p: PackedW4, bias: torch.Tensor | None, y: torch.Tensor) -> None:
     m, k = x2.shape
     z = p.zeros
-    _check(_lib.lib().fg_w4a16_gemm_cdna4(
+    L = _lib.lib()
+    ws_bytes = L.fg_w4a16_cdna4_workspace_bytes(m, p.n, k, p.group_size)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2.device) if ws_bytes else None
+    _check(L.fg_w4a16_gemm_cdna4(
         _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(p.qweight), _ld(p.qweight), _lib.ptr(p.scales),
         _lib.dtype_code(p.scales.dtype), _ld(p.scales), _lib.ptr(z), 0 if z is None else _ld(z), _lib.ptr(bias),
-        _code_or_zero(bias), _lib.ptr(y), y.stride(0), m, p.n, k, p.group_size, p.num_groups, _lib.stream_of(x2)),
-        "fg_w4a16_gemm_cdna4")
+        _code_or_zero(bias), _lib.ptr(y), y.stride(0), m, p.n, k, p.group_size, p.num_groups, _lib.ptr(ws), ws_bytes,
+        _lib.stream_of(x2)), "fg_w4a16_gemm_cdna4")
 
 
 def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = None, *,
@@ -369,8 +372,9 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     The C library picks the kernel per shape (``config={"impl": "gemv" | "mfma" | "prefill" | "generic", ...}`` or
     ``FORGE_W4_IMPL`` overrides it): split-K register GEMV for 1-2 rows (and small weights at 3-4), the skinny MFMA
     kernel up to 32 rows, dequantise-to-LDS MFMA tiles beyond, a per-element kernel for irregular act order or
-    unaligned weights.  A weight in the ``cdna4_mfma`` layout (``prepare_w4(p, CDNA4_W4)``) runs its own MFMA kernel
-    for 1..64 rows and a portable_row copy beyond.  Every kernel reduces in a fixed order, so results are run-to-run reproducible whatever
+    unaligned weights.  A weight in the ``cdna4_mfma`` layout (``prepare_w4(p, CDNA4_W4)``) runs its own MFMA kernels
+    for 1..64 rows (a register ring, or an LDS ring with a K-split reduce for 33..64 rows and long K) and a
+    portable_row copy beyond.  Every kernel reduces in a fixed order, so results are run-to-run reproducible whatever
     ``deterministic`` says.
     """
     _on_gpu(x, "w4a16_linear")

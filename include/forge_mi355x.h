@@ -119,12 +119,20 @@ size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
  * gfx950, over this build's fragment order (v_mfma_f32_16x16x32 B operands; load-time repack in
  * forge_amd.layouts.repack / ops_gemm.prepare_w4).  Same arguments and results as fg_w4a16_gemm except:
  *   qweight  int32 [ceil(N/16), ldq]: 16-channel tile rows, 256 words per 128-column tile, ldq >= 2 * K (K % 128 == 0)
- *   no perm / g_idx (act-order weights are column-sorted first), no workspace (one launch, slices summed in LDS)
+ *   no perm / g_idx (act-order weights are column-sorted first)
+ *   workspace  16-byte aligned, at least fg_w4a16_cdna4_workspace_bytes(M, N, K, group_size) bytes (NULL when that
+ *              is 0): fp32 K-split partials of the LDS-ring kernel (33..64 rows, or 9..64 over K >= 8192), summed by a
+ *              second launch in split order; smaller M runs one launch that sums its K slices in LDS
  * Needs group_size % 128 == 0 (or one group), fp16 / bf16 scales, 16-byte aligned x (ldx % 8 == 0) and qweight. */
 int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
                         const void* scales, int scale_dtype, int64_t lds, const int32_t* zeros, int64_t ldz,
                         const void* bias, int bias_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        int32_t group_size, int32_t n_groups, fg_stream_t stream);
+                        int32_t group_size, int32_t n_groups, void* workspace, size_t workspace_bytes,
+                        fg_stream_t stream);
+
+/* Workspace bytes fg_w4a16_gemm_cdna4 may need for this problem (an upper bound: 0 when its launch plan has no K
+ * split). */
+size_t fg_w4a16_cdna4_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
 
 /* Dense dequantisation out[n,k] = (q - z) * s computed in fp32 and rounded once to out_dtype (FG_F32|FG_F16|FG_BF16).
  * Replaces forge/kernels/triton/gemm_w4_dequant.py:143-191 (w4_dequant) and PackedW4.dequantize

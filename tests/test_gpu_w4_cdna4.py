@@ -2,7 +2,8 @@
 oracle: ragged N, one / several groups, symmetric and asymmetric weights, bf16 / fp16 x, fp16 / bf16 scales, bias,
 M from 1 to 64, the Llama-3-8B shapes at full size; weights repacked from portable_row at load time (a bit-exact
 permutation), the packed-linear module built in that layout, and calls its kernel does not take served by the
-portable copy.  Bar: max|y - ref| / max|ref| <= 1e-2 plus the reference's compare() rule."""
+portable copy; the LDS-ring kernel (33..64 rows, or 9..64 over K >= 8192) with and without its K-split reduce, and its
+workspace check.  Bar: max|y - ref| / max|ref| <= 1e-2 plus the reference's compare() rule."""
 from __future__ import annotations
 
 import pytest
@@ -78,5 +79,41 @@ def test_cdna4_module_and_c_abi_rejections():
     y = torch.empty(65, n, dtype=torch.bfloat16, device=DEV)
     rc = L_.fg_w4a16_gemm_cdna4(_lib.ptr(xx), k, _lib.BF16, _lib.ptr(p.qweight), p.qweight.stride(0), _lib.ptr(p.scales),
                                 _lib.F16, n, _lib.ptr(p.zeros), p.zeros.stride(0), None, 0, _lib.ptr(y), n, 65, n, k, 128,
-                                p.num_groups, _lib.stream_of(xx))
+                                p.num_groups, None, 0, _lib.stream_of(xx))
     assert rc == _lib.EUNSUPPORTED and "M <= 64" in _lib.last_error()
+    # the K-split plan of 64 rows over a long K needs its workspace
+    assert L_.fg_w4a16_cdna4_workspace_bytes(64, n, 8192, 128) > 0
+    assert L_.fg_w4a16_cdna4_workspace_bytes(16, n, 4096, 128) == 0
+
+
+# The LDS-ring kernel: 33..64 rows, or 9..64 rows over K >= 8192 (N % 16 == 0); K-split plans with a reduce launch
+# (small N, long K) and without (wide N), one group / several groups per step, symmetric, fp16 x, bf16 scales, bias.
+@pytest.mark.parametrize("m,n,k,gs", [(33, 2048, 4096, 128), (40, 4096, 4096, 256), (64, 1024, 2048, -1),
+                                      (64, 16384, 4096, 128), (48, 512, 8192, 128), (12, 4096, 8192, 256),
+                                      (16, 4096, 14336, 128), (24, 1024, 16384, -1), (64, 4096, 14336, 128)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_cdna4_ring_kernel(m, n, k, gs, xdt):
+    sdt = torch.bfloat16 if m % 2 else torch.float16
+    y, ref, _ = _case(m, n, k, gs, sym=(m % 3 == 0), xdt=xdt, sdt=sdt, bias=(m != 64), seed=m + k)
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"cdna4 ring m={m} n={n} k={k} gs={gs}")
+
+
+def test_cdna4_ring_reproducible_and_workspace_checked():
+    n, k = 4096, 14336
+    q, s, z = w4_parts(n, k, 128, False, seed=11)
+    p = ops.prepare_w4(L.pack_w4(q, s, z, 128).to(DEV), L.CDNA4_W4)
+    x = x_act(64, k, seed=12).to(DEV)
+    runs = [ops.w4a16_linear(x, p) for _ in range(3)]
+    assert all(torch.equal(runs[0], r) for r in runs[1:])
+    L_ = _lib.lib()
+    need = L_.fg_w4a16_cdna4_workspace_bytes(64, n, k, 128)
+    assert need > 0
+    y = torch.empty(64, n, dtype=torch.bfloat16, device=DEV)
+    args = (_lib.ptr(x), k, _lib.BF16, _lib.ptr(p.qweight), p.qweight.stride(0), _lib.ptr(p.scales), _lib.F16, n,
+            _lib.ptr(p.zeros), p.zeros.stride(0), None, 0, _lib.ptr(y), n, 64, n, k, 128, p.num_groups)
+    assert L_.fg_w4a16_gemm_cdna4(*args, None, 0, _lib.stream_of(x)) == _lib.EINVAL
+    assert "workspace" in _lib.last_error()
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    assert L_.fg_w4a16_gemm_cdna4(*args, _lib.ptr(ws), need - 16, _lib.stream_of(x)) == _lib.EINVAL
+    assert L_.fg_w4a16_gemm_cdna4(*args, _lib.ptr(ws), need, _lib.stream_of(x)) == _lib.OK
+    assert torch.equal(y, runs[0])

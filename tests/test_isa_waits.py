@@ -5,7 +5,9 @@ that later loads may stay in flight.  That is only correct while the instruction
 * w4_big_kernel (prefill, two register sets): the N loads after the last x load of a slice are the next weight
   fetch, so at least N vector-memory loads must follow the last `global_load_lds` before each such wait;
 * mm_ring_kernel (W8A8 small M, S-stage ring): each loop iteration issues exactly the NI direct-to-LDS loads of one
-  slice and no other vector-memory load, and waits with vmcnt((S - 2) * NI) ("slice kt + 1 has landed").
+  slice and no other vector-memory load, and waits with vmcnt((S - 2) * NI) ("slice kt + 1 has landed");
+* w4_ring_kernel (W4 on the CDNA4 layout, 33..64 rows or long K): the same rule with NI = 4 MB / BW + T + 2 buffer
+  loads into LDS per step.
 
 A compiler that reorders, splits or adds a load there breaks the check here, on the CPU, instead of silently racing on
 the GPU.  No GPU is used."""
@@ -90,8 +92,9 @@ def _vmem(mnem: str) -> bool:
     return mnem.startswith(("global_load", "buffer_load"))
 
 
-def _lds_dma(mnem: str) -> bool:
-    return _vmem(mnem) and "_lds" in mnem
+def _lds_dma(mnem: str, ops: str = "") -> bool:
+    """A direct-to-LDS load: global_load_lds_* or a buffer load with the lds modifier."""
+    return _vmem(mnem) and ("_lds" in mnem or re.search(r"\blds\b", ops.split("//")[0]) is not None)
 
 
 def _vmcnt(mnem: str, ops: str) -> int | None:
@@ -108,7 +111,7 @@ def _barrier_waits(code: list[tuple[int, str, str]]) -> list[tuple[int, int]]:
 
 def _dma_landed(code: list[tuple[int, str, str]], idx: int) -> bool:
     """Whether every direct-to-LDS load before code[idx] has landed once code[idx] (a vmcnt wait) retires."""
-    last_dma = max((i for i in range(idx) if _lds_dma(code[i][1])), default=None)
+    last_dma = max((i for i in range(idx) if _lds_dma(code[i][1], code[i][2])), default=None)
     if last_dma is None:
         return True
     # vmcnt(k) leaves only the k most recent loads in flight: the direct-to-LDS load has landed once some wait from it
@@ -138,10 +141,35 @@ def test_prefill_waits_leave_only_the_weight_fetch_in_flight(kernels):
         if "w4_big_kernel" not in name or not name.endswith("iiiii") or "Li2EEEv" not in name:
             continue
         for idx, n in _barrier_waits(code):
-            assert any(_lds_dma(m) for _, m, _ in code[:idx]), name
+            assert any(_lds_dma(m, o) for _, m, o in code[:idx]), name
             assert _dma_landed(code, idx), f"{name}: the vmcnt({n}) at {idx} leaves a direct-to-LDS load in flight"
             found += 1
     assert found >= 16, f"expected the two-register-set prefill instances, checked {found} waits"
+
+
+def _check_ring_loops(name: str, code: list[tuple[int, str, str]], ni: int, s: int) -> int:
+    """Every barrier wait of a ring kernel is vmcnt((S - 2) * NI), and the loop around it issues exactly NI
+    direct-to-LDS loads and no other vector-memory load.  Returns the loops checked."""
+    addr = {a: i for i, (a, _, _) in enumerate(code)}
+    waits = _barrier_waits(code)
+    assert waits and all(n == (s - 2) * ni for _, n in waits), (name, waits, ni, s)
+    found = 0
+    for wi, _ in waits:
+        # the loop around this wait: the first later branch whose target lies before the wait
+        for j in range(wi + 1, len(code)):
+            mnem, ops = code[j][1], code[j][2]
+            if mnem.startswith(("s_cbranch", "s_branch")):
+                tgt = re.search(r"<\S+\+0x([0-9a-f]+)>", ops)
+                base = code[0][0]
+                if tgt and base + int(tgt.group(1), 16) <= code[wi][0]:
+                    head = addr[base + int(tgt.group(1), 16)]
+                    body = code[head:j + 1]
+                    dma = sum(1 for _, m, o in body if _lds_dma(m, o))
+                    other = sum(1 for _, m, o in body if _vmem(m) and not _lds_dma(m, o))
+                    assert dma == ni and other == 0, f"{name}: loop issues {dma} DMA + {other} other loads"
+                    found += 1
+                    break
+    return found
 
 
 def test_ring_kernel_loop_issues_one_slice_and_waits_for_the_next(kernels):
@@ -150,23 +178,15 @@ def test_ring_kernel_loop_issues_one_slice_and_waits_for_the_next(kernels):
         if "mm_ring_kernel" not in name:
             continue
         bm, bn, wm, wn, s = (int(v) for v in re.findall(r"Li(\d+)E", name)[:5])
-        ni = (bm + bn) * 128 // 16 // (wm * wn * 64)
-        addr = {a: i for i, (a, _, _) in enumerate(code)}
-        waits = _barrier_waits(code)
-        assert waits and all(n == (s - 2) * ni for _, n in waits), (name, waits, ni, s)
-        for wi, _ in waits:
-            # the loop around this wait: the first later branch whose target lies before the wait
-            for j in range(wi + 1, len(code)):
-                mnem, ops = code[j][1], code[j][2]
-                if mnem.startswith(("s_cbranch", "s_branch")):
-                    tgt = re.search(r"<\S+\+0x([0-9a-f]+)>", ops)
-                    base = code[0][0]
-                    if tgt and base + int(tgt.group(1), 16) <= code[wi][0]:
-                        head = addr[base + int(tgt.group(1), 16)]
-                        body = code[head:j + 1]
-                        dma = sum(1 for _, m, _ in body if _lds_dma(m))
-                        other = sum(1 for _, m, _ in body if _vmem(m) and not _lds_dma(m))
-                        assert dma == ni and other == 0, f"{name}: loop issues {dma} DMA + {other} other loads"
-                        found += 1
-                        break
+        found += _check_ring_loops(name, code, (bm + bn) * 128 // 16 // (wm * wn * 64), s)
     assert found >= 4, f"expected the ring instances' loops, checked {found}"
+
+
+def test_w4_ring_kernel_loop_issues_one_step_and_waits_for_the_next(kernels):
+    found = 0
+    for name, code in kernels.items():
+        if "w4_ring_kernel" not in name:
+            continue
+        mb, t, bw, s = (int(v) for v in re.findall(r"Li(\d+)E", name)[:4])
+        found += _check_ring_loops(name, code, 4 * mb // bw + t + 2, s)
+    assert found >= 16, f"expected the W4 ring instances' loops, checked {found}"
