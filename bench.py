@@ -408,7 +408,7 @@ def load_traffic() -> dict | None:
         return None
     with open(path) as f:
         tr = json.load(f)
-    return tr if tr.get("kernel", "").split(" ")[0] == DOM_KERNEL.split("<")[0] else None
+    return tr if tr.get("kernel", "").split(" ")[0] == DOM_KERNEL else None
 
 
 def _cpu_model() -> str:

@@ -734,9 +734,11 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
   const int max_waves = w4_split_max_threads(mt) / kWave;
   if (ks > max_waves) return false;
   // One workgroup per CU when the channel blocks divide evenly (measured best on all four Llama-3-8B shapes; uneven
-  // counts such as 1.2-1.4 workgroups per CU cost up to 40%), else 8-16 wavefronts per workgroup.
+  // counts such as 1.2-1.4 workgroups per CU cost up to 40%), else the widest workgroup for wide outputs (gate+up, 3584
+  // blocks of 8 rows: 448 workgroups of 16 wavefronts 12.2 us against 12.6 for 896 of 8 and 14.4 for 1195 of 12) and
+  // 8-16 wavefronts otherwise.
   const int nblk = (N + r - 1) / r, cus = device_cus();
-  int bw = max(2, 8 / ks);
+  int bw = nblk >= 8 * cus ? max_waves / ks : max(2, 8 / ks);
   if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) bw = nblk / cus;
   while (bw * ks > max_waves && bw > 1) --bw;
   *S = s; *R = r; *KS = ks; *BW = bw;
