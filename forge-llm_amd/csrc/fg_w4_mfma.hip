@@ -193,8 +193,17 @@ __global__ void __launch_bounds__(256) w4_splitk_reduce_kernel(const float* __re
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t MN = (int64_t)M * N;
   if (t >= MN) return;
+  // fixed order; the partials are loaded four splits at a time before any is added (adding each as it arrives waits
+  // out one L2 round trip per split)
   float v = 0.f;
-  for (int s = 0; s < S; ++s) v += ws[s * MN + t];  // fixed order
+  for (int s = 0; s < S; s += 4) {
+    float p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p[u] = ws[(int64_t)min(s + u, S - 1) * MN + t];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s + u < S) v += p[u];
+  }
   const int m = (int)(t / N), n = (int)(t - (int64_t)m * N);
   if (bias) v += load_f(bias, bdt, n);
   y[(int64_t)m * ldy + n] = XBF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);

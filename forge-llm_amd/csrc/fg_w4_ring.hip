@@ -61,8 +61,6 @@ __device__ __forceinline__ uint4 rg_unpack(uint32_t w, uint32_t mask, uint32_t m
                     rg_and_or(w >> 12, mask, magic));
 }
 
-constexpr int kRingBW = 4;  // wavefronts per workgroup
-
 template <int MB, int T, int BW>
 struct RingShape {
   static_assert((4 * MB) % BW == 0, "the x rows of a step split evenly over the wavefronts");
@@ -234,7 +232,9 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
       }
 }
 
-// y[m, n .. n + 7] = sum over the KS partials in split order (+ bias), one thread per 8 outputs (N % 16 == 0)
+// y[m, n .. n + 7] = sum over the KS partials in split order (+ bias), one thread per 8 outputs (N % 16 == 0).  The
+// partials are loaded four splits at a time before any is added (a loop that adds each split as it arrives waits out
+// one L2 round trip per split: 4.2 us for 4 splits of a 64 x 4096 output), then summed in split order.
 template <bool XBF16>
 __global__ void __launch_bounds__(256) w4_ring_reduce_kernel(const float* __restrict__ part, int KS, int M, int N,
                                                              const void* __restrict__ bias, int bdt,
@@ -243,13 +243,24 @@ __global__ void __launch_bounds__(256) w4_ring_reduce_kernel(const float* __rest
   const int n8 = N / 8;
   if (idx >= (int64_t)M * n8) return;
   const int m = (int)(idx / n8), n = (int)(idx - (int64_t)m * n8) * 8;
-  const int64_t MN = (int64_t)M * N;
+  const int64_t MN4 = (int64_t)M * N / 4;
   f32x4_rg_t a = f32x4_rg_t{0.f, 0.f, 0.f, 0.f}, b = a;
   const f32x4_rg_t* p = reinterpret_cast<const f32x4_rg_t*>(part + (int64_t)m * N + n);
-  for (int k = 0; k < KS; ++k) {
-    a += p[0];
-    b += p[1];
-    p += MN / 4;
+  for (int k = 0; k < KS; k += 4) {
+    f32x4_rg_t va[4], vb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // past the last split: re-read it, and add nothing below
+      const int64_t o = (int64_t)min(k + u, KS - 1) * MN4;
+      va[u] = p[o];
+      vb[u] = p[o + 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (k + u < KS) {
+        a += va[u];
+        b += vb[u];
+      }
+    }
   }
   float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   uint16_t h[8];
@@ -279,15 +290,16 @@ bool w4_ring_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, cons
 }
 
 // Launch shape, from a sweep of (BW, T, KS) against the register-ring kernel (w4_frag_kernel) on the Llama-3-8B
-// shapes at M = 1 / 16 / 32 / 64 (graph replays over a 1.2 GB weight ring): BW = 4 wavefronts; T = 2 tiles per
+// shapes at M = 1 / 16 / 32 / 64 (graph replays over a 1.2 GB weight ring): BW = 4 or 8 wavefronts; T = 2 tiles per
 // wavefront for 33..64 rows over at least 1024 tiles (gate+up: 37.9 us against 43.2 with one), else 1; KS = 1 when the
-// channel groups fill three quarters of the CUs, else the smallest power of two that fills them, doubled while a split
-// is longer than 16 steps over K >= 8192 (down: 8 splits of 14 steps, 26.0 us at M = 64 against 30.7 with 4).
+// channel groups fill three quarters of the CUs, else the smallest power of two that gives one wavefront per SIMD,
+// doubled while a split is longer than 16 steps over K >= 8192 (down: 8 splits of 14 steps, 26.0 us at M = 64 against
+// 30.7 with 4).
 // Measured (us, this kernel + reduce / w4_frag_kernel): M = 64 qkv 18.4 / 21.2, o_proj 14.7 / 18.8, gate+up 37.9 /
 // 44.0, down 26.0 / 54.7; M = 32 down 18.7 / 29.9; M = 16 down 15.9 / 17.0.  Below that the register ring is as fast
 // or faster (w4_ring_preferred).
 struct RingPlan {
-  int mb, T, KS, ngrp;
+  int mb, T, BW, KS, ngrp;
 };
 
 static RingPlan w4_ring_plan(int M, int N, int K) {
@@ -295,10 +307,13 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int NT = N / 16, nsteps = K / 128, cus = device_cus();
   p.T = p.mb == 4 && NT >= 1024 ? 2 : 1;
-  p.ngrp = (NT + kRingBW * p.T - 1) / (kRingBW * p.T);
+  // eight wavefronts (x shared by 128 channels) for 33..64 rows over one-tile wavefronts on qkv-sized or long-K
+  // weights: qkv M = 64 17.1 us against 18.5, down 25.7 against 28.2; o_proj 15.7 against 14.6 stays on four
+  p.BW = p.mb == 4 && p.T == 1 && (NT >= 384 || nsteps >= 64) ? 8 : 4;
+  p.ngrp = (NT + p.BW * p.T - 1) / (p.BW * p.T);
   int ks = 1;
   if (4 * p.ngrp < 3 * cus)
-    while (p.ngrp * ks < cus && 2 * ks <= nsteps) ks *= 2;
+    while (p.ngrp * ks * p.BW < 4 * cus && 2 * ks <= nsteps) ks *= 2;
   if (nsteps >= 64)
     while (nsteps / ks > 16 && p.ngrp * ks < 4 * cus && 2 * ks <= nsteps) ks *= 2;
   p.KS = ks;
@@ -344,9 +359,10 @@ static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
 
 template <bool XBF16, bool SBF16>
 static hipError_t launch_ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
-  if (p.mb == 1) return launch_ring_t<1, 1, kRingBW, 4, XBF16, SBF16>(a, s);
-  if (p.mb == 2) return launch_ring_t<2, 1, kRingBW, 3, XBF16, SBF16>(a, s);
-  return p.T == 2 ? launch_ring_t<4, 2, kRingBW, 3, XBF16, SBF16>(a, s) : launch_ring_t<4, 1, kRingBW, 3, XBF16, SBF16>(a, s);
+  if (p.mb == 1) return launch_ring_t<1, 1, 4, 4, XBF16, SBF16>(a, s);
+  if (p.mb == 2) return launch_ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
+  if (p.T == 2) return launch_ring_t<4, 2, 4, 3, XBF16, SBF16>(a, s);
+  return p.BW == 8 ? launch_ring_t<4, 1, 8, 3, XBF16, SBF16>(a, s) : launch_ring_t<4, 1, 4, 3, XBF16, SBF16>(a, s);
 }
 
 hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
