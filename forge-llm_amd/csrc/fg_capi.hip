@@ -60,14 +60,14 @@ bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int 
 hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
                           int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
                           int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, hipStream_t s);
-bool w4_ring_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
-                const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
+bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
+                int64_t lds, const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
 bool w4_ring_preferred(int M, int K);
 size_t w4_ring_workspace_bytes(int M, int N, int K);
-hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
-                          int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
-                          int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
-                          hipStream_t s);
+hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
+                          const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias,
+                          int bdt, void* y, int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws,
+                          size_t ws_bytes, hipStream_t s);
 hipError_t launch_w4_gemv_tile(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
                                const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz,
                                const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
@@ -225,6 +225,15 @@ namespace {
 // the prefill kernel from 48 rows (gate+up at M = 64: 1.10 against 0.60 TB/s).
 constexpr int64_t kPrefillMinM = 33;
 
+// Whether the automatic policy sends a 9..64-row call to the LDS-ring kernel (portable_row weights): 33..64 rows, or
+// 9..64 over K >= 8192 (measured on the Llama-3-8B shapes, us, ring / previous choice: M = 64 qkv 17.8 / 22.4,
+// o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 16 down 14.4 / 20.3), when its shape conditions can
+// hold (N % 16 == 0, K % 128 == 0, group % 128 == 0 or one group); the operands decide the rest at launch.
+bool ring_policy(const fg_w4_config* cfg, int64_t M, int64_t N, int64_t K) {
+  return (!cfg || (cfg->impl == FG_W4_AUTO && !cfg->tile_m && !cfg->split_k)) && M <= 64 && N % 16 == 0 &&
+         K % 128 == 0 && fg::w4_ring_preferred((int)M, (int)K);
+}
+
 // Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
 // workspace a caller sizes is the workspace the launch uses.
 struct W4Plan {
@@ -286,6 +295,11 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
     if (prefill_ok) {
       const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits);
       if (wb > p->ws_bytes) p->ws_bytes = wb;
+    }
+    // ... and for the LDS-ring kernel the launch takes for 33..64 rows (9..64 over K >= 8192) when it applies
+    if (ring_policy(cfg, M, N, K)) {
+      const size_t wr = fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+      if (wr > p->ws_bytes) p->ws_bytes = wr;
     }
   }
   return FG_OK;
@@ -379,12 +393,22 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
                         fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K,
                                          gs, G);
     const bool big = fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G) && !(cfg && cfg->tile_m);
-    int kern = 0;  // 0: LDS-tiled MFMA, 1: skinny, 2: prefill
+    int kern = 0;  // 0: LDS-tiled MFMA, 1: skinny, 2: prefill, 3: LDS ring
     if (p.impl == FG_W4_PREFILL)
       kern = (auto_impl && skinny && M <= 64 && N <= 4096 && K <= 4096) ? 1 : (big ? 2 : 0);
     else
       kern = skinny ? 1 : ((auto_impl && big) ? 2 : 0);
-    if (kern == 1)
+    if (ring_policy(cfg, M, N, K) && perm == nullptr &&
+        fg::w4_ring_ok(true, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs,
+                       G) &&
+        (fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K) == 0 ||
+         (workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0)))
+      kern = 3;
+    if (kern == 3)
+      e = fg::launch_w4_ring(true, x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias,
+                             bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G, workspace,
+                             workspace_bytes, s);
+    else if (kern == 1)
       e = fg::launch_w4_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
                                ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
     else if (kern == 2)
@@ -492,12 +516,13 @@ int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* 
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_cdna4: needs M <= 64, K %% 128 == 0, group %% 128 == 0 (or one group), "
                                  "16-bit scales, 16-byte aligned x and qweight, ldx %% 8 == 0, ldq %% 4 == 0");
   if (fg::w4_ring_preferred((int)M, (int)K) &&
-      fg::w4_ring_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs, G)) {
+      fg::w4_ring_ok(false, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs,
+                     G)) {
     const size_t need = fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
       return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: needs a 16-byte aligned workspace of %zu bytes, got %zu", need,
                   workspace ? workspace_bytes : (size_t)0);
-    return hip_status(fg::launch_w4_ring(x, ldx, x_dtype == FG_BF16, qweight, ldq, scales, scale_dtype, lds, zeros,
+    return hip_status(fg::launch_w4_ring(false, x, ldx, x_dtype == FG_BF16, qweight, ldq, scales, scale_dtype, lds, zeros,
                                          ldz, bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G,
                                          workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
                       "fg_w4a16_gemm_cdna4 launch");

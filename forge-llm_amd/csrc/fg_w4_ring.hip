@@ -61,6 +61,16 @@ __device__ __forceinline__ uint4 rg_unpack(uint32_t w, uint32_t mask, uint32_t m
                     rg_and_or(w >> 12, mask, magic));
 }
 
+// portable_row word (nibble t = column t) -> the same four pairs in column order: byte p of w and of w >> 4 moved to
+// bytes 0 and 2 by one v_perm_b32 (bytes 1 and 3 zero), then masked and tagged (nibble 2p | magic, 2p + 1 | magic)
+__device__ __forceinline__ uint4 rg_unpack_portable(uint32_t w, uint32_t mask, uint32_t magic) {
+  const uint32_t h = w >> 4;
+  return make_uint4(rg_and_or(__builtin_amdgcn_perm(h, w, 0x0C040C00u), mask, magic),
+                    rg_and_or(__builtin_amdgcn_perm(h, w, 0x0C050C01u), mask, magic),
+                    rg_and_or(__builtin_amdgcn_perm(h, w, 0x0C060C02u), mask, magic),
+                    rg_and_or(__builtin_amdgcn_perm(h, w, 0x0C070C03u), mask, magic));
+}
+
 template <int MB, int T, int BW>
 struct RingShape {
   static_assert((4 * MB) % BW == 0, "the x rows of a step split evenly over the wavefronts");
@@ -89,7 +99,12 @@ struct RingArgs {
   uint32_t qbytes, xbytes, sbytes, zbytes;
 };
 
-template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+// PORT: weights in portable_row ([N, ldq] int32 words, row n = channel n): a tile's step is 16 rows x 64 bytes,
+// loaded into LDS row by row with the 16-byte quarter q of row r at position q ^ ((r / 4) % 4) (the 16 rows of one
+// B read fall on distinct bank groups), and lane group j takes quarter j: MFMA k-step s of lane group j is word 4 j + s
+// (columns 32 j + 8 s ..), so x's unit 4 j + s goes with it (the sum over K does not care which 32 columns go to
+// which k-step).  Otherwise the CDNA4 layout: lane l's 16 bytes at l * 16, k-step s = word s (columns 32 s + 8 j ..).
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
 __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   using Sh = RingShape<MB, T, BW>;
   static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
@@ -121,8 +136,16 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   }
   uint32_t wv[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-    wv[t] = tile0 + t < NT ? (uint32_t)(tile0 + t) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)lane : a.qbytes;
+  for (int t = 0; t < T; ++t) {
+    if constexpr (PORT) {  // LDS position lane = row lane / 4, slot lane % 4, holding quarter slot ^ (row / 4 % 4)
+      const int row = lane >> 2, quarter = (lane & 3) ^ ((lane >> 4) & 3);
+      wv[t] = tile0 + t < NT
+                  ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)quarter
+                  : a.qbytes;
+    } else {
+      wv[t] = tile0 + t < NT ? (uint32_t)(tile0 + t) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)lane : a.qbytes;
+    }
+  }
   // scales: lane i < 8 T loads the channel pair 2i, 2i + 1 of the wavefront's tiles; zero words: lane i < 2 T loads
   // word i (eight channels each)
   const bool sl = lane < 8 * T && tile0 + lane / 8 < NT, zl = lane < 2 * T && tile0 + lane / 2 < NT;
@@ -144,7 +167,7 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(q_, (lds_void_t*)(stg + Sh::X + (wave * T + t) * 1024), 16,
-                                               (int)wv[t], st * 1024, 0, 2);
+                                               (int)wv[t], st * (PORT ? 64 : 1024), 0, 2);
     // the group row goes into the per-lane offset (past-the-end lanes must stay past the end)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(s_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * 512), 4,
                                              sl ? (int)(g * lds2 + sv) : (int)a.sbytes, 0, 0, 0);
@@ -168,7 +191,8 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
     float sc[T], zb[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      raw[t] = *reinterpret_cast<const uint4*>(sw + (wave * T + t) * 1024 + lane * 16);
+      const int wpos = PORT ? r16 * 64 + ((j ^ ((r16 >> 2) & 3)) * 16) : lane * 16;
+      raw[t] = *reinterpret_cast<const uint4*>(sw + (wave * T + t) * 1024 + wpos);
       const uint16_t sb = reinterpret_cast<const uint16_t*>(ssz)[t * 16 + r16];
       sc[t] = SBF16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
       const uint32_t zw = reinterpret_cast<const uint32_t*>(ssz + 256)[t * 2 + (r16 >> 3)];
@@ -179,7 +203,8 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
       uint4 af[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        af[s] = *reinterpret_cast<const uint4*>(stg + (16 * i + r16) * 256 + (((4 * s + j) ^ r16) * 16));
+        af[s] = *reinterpret_cast<const uint4*>(stg + (16 * i + r16) * 256 +
+                                                (((PORT ? 4 * j + s : 4 * s + j) ^ r16) * 16));
       f32x4_rg_t xs = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) xs = rg_mfma<XBF16>(af[s], ones, xs);
@@ -188,7 +213,9 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
         const uint32_t wq[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
         f32x4_rg_t as = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) as = rg_mfma<XBF16>(af[s], rg_unpack(wq[s], mask, magic), as);
+        for (int s = 0; s < 4; ++s)
+          as = rg_mfma<XBF16>(af[s], PORT ? rg_unpack_portable(wq[s], mask, magic) : rg_unpack(wq[s], mask, magic),
+                              as);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[t][i][e] = __builtin_fmaf(sc[t], __builtin_fmaf(-zb[t], xs[e], as[e]), acc[t][i][e]);
@@ -279,14 +306,16 @@ __global__ void __launch_bounds__(256) w4_ring_reduce_kernel(const float* __rest
   }
 }
 
-bool w4_ring_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
-                const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G) {
+// portable: qweight [N, ldq] int32 (ldq >= K / 8); otherwise the CDNA4 tile rows [N / 16, ldq] (ldq >= 2 K)
+bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
+                int64_t lds, const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G) {
   const int64_t k2g = 1LL << 31;  // offsets past a span plus a step offset stay below 2^32
+  const int64_t qspan = portable ? N * ldq * 4 : (N / 16) * ldq * 4;
   return M > 0 && M <= 64 && sdt != FG_F32 && N % 16 == 0 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) &&
-         (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && ldq >= 2 * K &&
-         (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
+         (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 &&
+         ldq >= (portable ? K / 8 : 2 * K) && (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
          (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && (reinterpret_cast<uintptr_t>(zeros) % 4) == 0 &&
-         (N / 16) * ldq * 4 < k2g && (int64_t)M * ldx * 2 < k2g && G * lds * 2 < k2g && G * ldz * 4 < k2g;
+         qspan < k2g && (int64_t)M * ldx * 2 < k2g && G * lds * 2 < k2g && G * ldz * 4 < k2g;
 }
 
 // Launch shape, from a sweep of (BW, T, KS) against the register-ring kernel (w4_frag_kernel) on the Llama-3-8B
@@ -343,11 +372,11 @@ static hipError_t launch_ring_reduce(bool xbf16, const float* part, int KS, int 
   return hipGetLastError();
 }
 
-template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
 static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
   using Sh = RingShape<MB, T, BW>;
   const size_t shm = (size_t)S * Sh::STAGE;
-  auto kern = w4_ring_kernel<MB, T, BW, S, XBF16, SBF16>;
+  auto kern = w4_ring_kernel<MB, T, BW, S, XBF16, SBF16, PORT>;
   if (shm > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -357,15 +386,23 @@ static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <bool XBF16, bool SBF16>
+template <bool XBF16, bool SBF16, bool PORT>
 static hipError_t launch_ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
-  if (p.mb == 1) return launch_ring_t<1, 1, 4, 4, XBF16, SBF16>(a, s);
-  if (p.mb == 2) return launch_ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
-  if (p.T == 2) return launch_ring_t<4, 2, 4, 3, XBF16, SBF16>(a, s);
-  return p.BW == 8 ? launch_ring_t<4, 1, 8, 3, XBF16, SBF16>(a, s) : launch_ring_t<4, 1, 4, 3, XBF16, SBF16>(a, s);
+  if (p.mb == 1) return launch_ring_t<1, 1, 4, 4, XBF16, SBF16, PORT>(a, s);
+  if (p.mb == 2) return launch_ring_t<2, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
+  if (p.T == 2) return launch_ring_t<4, 2, 4, 3, XBF16, SBF16, PORT>(a, s);
+  return p.BW == 8 ? launch_ring_t<4, 1, 8, 3, XBF16, SBF16, PORT>(a, s)
+                   : launch_ring_t<4, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
 }
 
-hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+template <bool PORT>
+static hipError_t launch_ring_p(bool xbf16, bool sbf, const RingPlan& p, const RingArgs& a, hipStream_t s) {
+  if (xbf16) return sbf ? launch_ring_x<true, true, PORT>(p, a, s) : launch_ring_x<true, false, PORT>(p, a, s);
+  return sbf ? launch_ring_x<false, true, PORT>(p, a, s) : launch_ring_x<false, false, PORT>(p, a, s);
+}
+
+hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
+                          const void* scales,
                           int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
                           int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
                           hipStream_t s) {
@@ -390,7 +427,7 @@ hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t*
   a.gsteps = single_group ? 0 : gs / 128;
   a.KS = p.KS;
   a.ngrp = p.ngrp;
-  a.qbytes = (uint32_t)((int64_t)(N / 16) * ldq * 4);
+  a.qbytes = (uint32_t)((int64_t)(portable ? N : N / 16) * ldq * 4);
   a.xbytes = (uint32_t)((int64_t)M * ldx * 2);
   a.sbytes = (uint32_t)((int64_t)G * lds * 2);
   a.zbytes = zeros ? (uint32_t)((int64_t)G * ldz * 4) : 0u;
@@ -399,12 +436,7 @@ hipError_t launch_w4_ring(const void* x, int64_t ldx, bool xbf16, const int32_t*
                    reinterpret_cast<uintptr_t>(ws) % 16 != 0))
     return hipErrorInvalidValue;
   const bool sbf = sdt == FG_BF16;
-  hipError_t e;
-  if (xbf16) {
-    e = sbf ? launch_ring_x<true, true>(p, a, s) : launch_ring_x<true, false>(p, a, s);
-  } else {
-    e = sbf ? launch_ring_x<false, true>(p, a, s) : launch_ring_x<false, false>(p, a, s);
-  }
+  const hipError_t e = portable ? launch_ring_p<true>(xbf16, sbf, p, a, s) : launch_ring_p<false>(xbf16, sbf, p, a, s);
   if (e != hipSuccess || p.KS == 1) return e;
   return launch_ring_reduce(xbf16, a.part, p.KS, M, N, bias, bdt, y, ldy, s);
 }

@@ -1,6 +1,6 @@
 """GPU parity of the kernels the automatic per-shape policy picks at the configs' full sizes, where no other test
-forces them: W4A16 (and W8A16) at 33..64 rows over the Llama-3-8B linears (64-row dequantise-to-LDS tiles plus the
-fixed-order split-K reduce), W4A16 at 4 rows over gate+up (skinny MFMA kernel), 256-row prefill tiles with fp16 x,
+forces them: W4A16 at 33..64 rows over the Llama-3-8B linears (the LDS-ring kernel plus its split-K reduce; the
+64-row dequantise-to-LDS prefill tiles, forced, beside it), W8A16 at 33..64 rows, W4A16 at 4 rows over gate+up (skinny MFMA kernel), 256-row prefill tiles with fp16 x,
 and INT8 W8A8 at configs[4]'s (K, N) = (8192, 57344) and (28672, 8192) for M = 1 and 4096.
 
 Bars: W4/W8A16 within max|y - ref| / max|ref| <= 1e-2 of the fp32 oracle plus the reference's compare() rule;
@@ -35,8 +35,9 @@ def _rows_oracle(xs: list[torch.Tensor], packed: dict) -> list[np.ndarray]:
 
 @pytest.mark.parametrize("shape", sorted(LLAMA))
 def test_w4_policy_33_to_64_rows_full_size(shape):
-    """M in {33, 48, 64}: the policy runs the prefill kernel with 64-row tiles and K splits (second launch: the
-    split-K reduce).  Forcing impl=prefill picks the same kernel, so both results are equal bit for bit."""
+    """M in {33, 48, 64}: the policy runs the LDS-ring kernel (K splits summed by a second launch), forcing
+    impl=prefill the 64-row prefill tiles with their split-K reduce; both against the oracle, the policy's result
+    reproducible run to run."""
     k, n = LLAMA[shape]
     q, s, z = w4_parts(n, k, 128, False, seed=k + n)
     p = L.pack_w4(q, s, z, 128).to(DEV)
@@ -51,8 +52,9 @@ def test_w4_policy_33_to_64_rows_full_size(shape):
         assert ops.last_path("w4a16_linear") == "hip"
         r = ref if b is None else (ref + to_f32(b)).astype(np.float32)
         assert_close(y.cpu(), r, ODT[xdt], what=f"w4 policy {shape} m={m}")
+        assert torch.equal(y, ops.w4a16_linear(x.to(DEV), p, bd)), f"{shape} m={m}: policy not reproducible"
         yf = ops.w4a16_linear(x.to(DEV), p, bd, config={"impl": "prefill"})
-        assert torch.equal(y, yf), f"{shape} m={m}: policy and forced prefill differ"
+        assert_close(yf.cpu(), r, ODT[xdt], what=f"w4 forced prefill {shape} m={m}")
 
 
 def test_w4_policy_64_rows_symmetric_qkv():
