@@ -62,8 +62,8 @@ hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t*
                           int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, hipStream_t s);
 bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
                 int64_t lds, const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
-bool w4_ring_preferred(int M, int K);
-size_t w4_ring_workspace_bytes(int M, int N, int K);
+bool w4_ring_preferred(bool portable, int M, int N, int K);
+size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K);
 hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
                           const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias,
                           int bdt, void* y, int64_t ldy, int M, int N, int K, int gs, bool single_group, int G, void* ws,
@@ -225,13 +225,14 @@ namespace {
 // the prefill kernel from 48 rows (gate+up at M = 64: 1.10 against 0.60 TB/s).
 constexpr int64_t kPrefillMinM = 33;
 
-// Whether the automatic policy sends a 9..64-row call to the LDS-ring kernel (portable_row weights): 33..64 rows, or
-// 9..64 over K >= 8192 (measured on the Llama-3-8B shapes, us, ring / previous choice: M = 64 qkv 17.8 / 22.4,
-// o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 16 down 14.4 / 20.3), when its shape conditions can
-// hold (N % 16 == 0, K % 128 == 0, group % 128 == 0 or one group); the operands decide the rest at launch.
+// Whether the automatic policy sends a 9..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
+// 13..16 over N >= 16384 and 9..12 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
+// / previous choice: M = 64 qkv 17.8 / 22.4, o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 32
+// gate+up 31.4 / 44.4; M = 16 down 14.4 / 20.3), when its shape conditions can hold (N % 16 == 0, K % 128 == 0,
+// group % 128 == 0 or one group); the operands decide the rest at launch.
 bool ring_policy(const fg_w4_config* cfg, int64_t M, int64_t N, int64_t K) {
   return (!cfg || (cfg->impl == FG_W4_AUTO && !cfg->tile_m && !cfg->split_k)) && M <= 64 && N % 16 == 0 &&
-         K % 128 == 0 && fg::w4_ring_preferred((int)M, (int)K);
+         K % 128 == 0 && fg::w4_ring_preferred(true, (int)M, (int)N, (int)K);
 }
 
 // Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
@@ -296,9 +297,9 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
       const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits);
       if (wb > p->ws_bytes) p->ws_bytes = wb;
     }
-    // ... and for the LDS-ring kernel the launch takes for 33..64 rows (9..64 over K >= 8192) when it applies
+    // ... and for the LDS-ring kernel when the policy sends the call there
     if (ring_policy(cfg, M, N, K)) {
-      const size_t wr = fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+      const size_t wr = fg::w4_ring_workspace_bytes(true, (int)M, (int)N, (int)K);
       if (wr > p->ws_bytes) p->ws_bytes = wr;
     }
   }
@@ -401,7 +402,7 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
     if (ring_policy(cfg, M, N, K) && perm == nullptr &&
         fg::w4_ring_ok(true, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs,
                        G) &&
-        (fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K) == 0 ||
+        (fg::w4_ring_workspace_bytes(true, (int)M, (int)N, (int)K) == 0 ||
          (workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0)))
       kern = 3;
     if (kern == 3)
@@ -484,7 +485,7 @@ int fg_w4a16_gemm_noalloc(const void* x, int64_t ldx, int x_dtype, const int32_t
 size_t fg_w4a16_cdna4_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size) {
   (void)group_size;
   if (M <= 0 || M > 64 || N <= 0 || K <= 0 || N >= kMaxDim || K >= kMaxDim) return 0;
-  return fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+  return fg::w4_ring_workspace_bytes(false, (int)M, (int)N, (int)K);
 }
 
 int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
@@ -515,10 +516,10 @@ int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* 
   if (!fg::w4_frag_ok(x, ldx, qweight, ldq, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K, gs, G))
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_cdna4: needs M <= 64, K %% 128 == 0, group %% 128 == 0 (or one group), "
                                  "16-bit scales, 16-byte aligned x and qweight, ldx %% 8 == 0, ldq %% 4 == 0");
-  if (fg::w4_ring_preferred((int)M, (int)K) &&
+  if (fg::w4_ring_preferred(false, (int)M, (int)N, (int)K) &&
       fg::w4_ring_ok(false, x, ldx, qweight, ldq, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, (int)M, N, K, gs,
                      G)) {
-    const size_t need = fg::w4_ring_workspace_bytes((int)M, (int)N, (int)K);
+    const size_t need = fg::w4_ring_workspace_bytes(false, (int)M, (int)N, (int)K);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16))
       return fail(FG_EINVAL, "fg_w4a16_gemm_cdna4: needs a 16-byte aligned workspace of %zu bytes, got %zu", need,
                   workspace ? workspace_bytes : (size_t)0);

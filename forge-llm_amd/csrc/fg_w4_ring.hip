@@ -326,7 +326,7 @@ bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, in
 // 30.7 with 4).
 // Measured (us, this kernel + reduce / w4_frag_kernel): M = 64 qkv 18.4 / 21.2, o_proj 14.7 / 18.8, gate+up 37.9 /
 // 44.0, down 26.0 / 54.7; M = 32 down 18.7 / 29.9; M = 16 down 15.9 / 17.0.  Below that the register ring is as fast
-// or faster (w4_ring_preferred).
+// or faster on the CDNA4 layout (w4_ring_preferred).
 struct RingPlan {
   int mb, T, BW, KS, ngrp;
 };
@@ -349,10 +349,17 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   return p;
 }
 
-bool w4_ring_preferred(int M, int K) { return M > 32 || (M > 8 && K >= 8192); }
+// CDNA4 layout: 33..64 rows, and 9..32 over K >= 8192; below that the register ring is as fast or faster.
+// portable_row: also 17..32 rows, and 13..16 rows over wide outputs, where the ring replaces the skinny kernel (us,
+// ring / skinny: M = 32 qkv 13.4 / 14.5, o_proj 11.1 / 12.2, gate+up 31.4 / 44.4; M = 24 gate+up 30.1 / 38.8; M = 16
+// gate+up 23.6 / 25.9, qkv 11.0 / 10.0).
+bool w4_ring_preferred(bool portable, int M, int N, int K) {
+  if (M > 32 || (M > 8 && K >= 8192)) return true;
+  return portable && (M > 16 || (M > 12 && N >= 16384));
+}
 
-size_t w4_ring_workspace_bytes(int M, int N, int K) {
-  if (M <= 0 || M > 64 || N % 16 != 0 || K % 128 != 0 || !w4_ring_preferred(M, K)) return 0;
+size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K) {
+  if (M <= 0 || M > 64 || N % 16 != 0 || K % 128 != 0 || !w4_ring_preferred(portable, M, N, K)) return 0;
   const RingPlan p = w4_ring_plan(M, N, K);
   return p.KS == 1 ? 0 : (size_t)p.KS * M * N * sizeof(float);
 }

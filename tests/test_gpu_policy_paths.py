@@ -1,6 +1,7 @@
 """GPU parity of the kernels the automatic per-shape policy picks at the configs' full sizes, where no other test
 forces them: W4A16 at 33..64 rows over the Llama-3-8B linears (the LDS-ring kernel plus its split-K reduce; the
-64-row dequantise-to-LDS prefill tiles, forced, beside it), W8A16 at 33..64 rows, W4A16 at 4 rows over gate+up (skinny MFMA kernel), 256-row prefill tiles with fp16 x,
+64-row dequantise-to-LDS prefill tiles, forced, beside it) and at 13..32 rows (the LDS-ring kernel; the skinny MFMA
+kernel, forced, beside it), W8A16 at 33..64 rows, W4A16 at 4 rows over gate+up (skinny MFMA kernel), 256-row prefill tiles with fp16 x,
 and INT8 W8A8 at configs[4]'s (K, N) = (8192, 57344) and (28672, 8192) for M = 1 and 4096.
 
 Bars: W4/W8A16 within max|y - ref| / max|ref| <= 1e-2 of the fp32 oracle plus the reference's compare() rule;
@@ -55,6 +56,30 @@ def test_w4_policy_33_to_64_rows_full_size(shape):
         assert torch.equal(y, ops.w4a16_linear(x.to(DEV), p, bd)), f"{shape} m={m}: policy not reproducible"
         yf = ops.w4a16_linear(x.to(DEV), p, bd, config={"impl": "prefill"})
         assert_close(yf.cpu(), r, ODT[xdt], what=f"w4 forced prefill {shape} m={m}")
+
+
+@pytest.mark.parametrize("shape", ["qkv", "o_proj", "gate_up"])
+def test_w4_policy_13_to_32_rows_full_size(shape):
+    """17..32 rows (13..16 over gate+up's 28672 channels): the policy runs the LDS-ring kernel on portable_row
+    weights; forcing impl=mfma runs the skinny kernel.  Both against the oracle, the policy's result reproducible."""
+    k, n = {"o_proj": (4096, 4096), **LLAMA}[shape]
+    q, s_, z = w4_parts(n, k, 128, False, seed=k + n + 1)
+    p = L.pack_w4(q, s_, z, 128).to(DEV)
+    cases = [(17, torch.bfloat16, True), (24, torch.float16, False), (32, torch.bfloat16, False)]
+    if shape == "gate_up":
+        cases.append((13, torch.float16, True))
+    xs = [x_act(m, k, xdt, seed=m + 5 * i) for i, (m, xdt, _) in enumerate(cases)]
+    refs = _rows_oracle(xs, oracle_packed(q, s_, z, 128))
+    for (m, xdt, has_b), x, ref in zip(cases, xs, refs):
+        b = (torch.randn(n, generator=gen(m + 1)) * 0.5).to(xdt) if has_b else None
+        bd = None if b is None else b.to(DEV)
+        y = ops.w4a16_linear(x.to(DEV), p, bd)
+        assert ops.last_path("w4a16_linear") == "hip"
+        r = ref if b is None else (ref + to_f32(b)).astype(np.float32)
+        assert_close(y.cpu(), r, ODT[xdt], what=f"w4 policy {shape} m={m}")
+        assert torch.equal(y, ops.w4a16_linear(x.to(DEV), p, bd)), f"{shape} m={m}: policy not reproducible"
+        yf = ops.w4a16_linear(x.to(DEV), p, bd, config={"impl": "mfma"})
+        assert_close(yf.cpu(), r, ODT[xdt], what=f"w4 forced skinny {shape} m={m}")
 
 
 def test_w4_policy_64_rows_symmetric_qkv():
