@@ -147,29 +147,80 @@ def test_prefill_waits_leave_only_the_weight_fetch_in_flight(kernels):
     assert found >= 16, f"expected the two-register-set prefill instances, checked {found} waits"
 
 
+def _successors(code: list[tuple[int, str, str]], addr: dict[int, int], i: int) -> list[int]:
+    """Indices control can reach from code[i] (branch targets resolved from the disassembler's <func+0xoff>)."""
+    mnem, ops = code[i][1], code[i][2]
+    if mnem == "s_endpgm":
+        return []
+    nxt = [i + 1] if i + 1 < len(code) else []
+    if mnem.startswith(("s_cbranch", "s_branch")):
+        tgt = re.search(r"<\S+\+0x([0-9a-f]+)>", ops)
+        t = [addr[code[0][0] + int(tgt.group(1), 16)]] if tgt else []
+        return t if mnem.startswith("s_branch") else nxt + t
+    return nxt
+
+
 def _check_ring_loops(name: str, code: list[tuple[int, str, str]], ni: int, s: int) -> int:
-    """Every barrier wait of a ring kernel is vmcnt((S - 2) * NI), and the loop around it issues exactly NI
-    direct-to-LDS loads and no other vector-memory load.  Returns the loops checked."""
+    """Every barrier wait of a ring kernel is vmcnt((S - 2) * NI); every path from kernel entry to the first wait issues
+    (S - 1) * NI direct-to-LDS loads, and every path from one wait to the next exactly NI (one step's; however the
+    compiler lays out or unrolls the loop) and no other vector-memory load, so each wait leaves exactly the S - 2
+    younger steps in flight; a path from the last wait to the end issues one step's loads or none.  Returns the waits
+    checked."""
     addr = {a: i for i, (a, _, _) in enumerate(code)}
     waits = _barrier_waits(code)
     assert waits and all(n == (s - 2) * ni for _, n in waits), (name, waits, ni, s)
-    found = 0
-    for wi, _ in waits:
-        # the loop around this wait: the first later branch whose target lies before the wait
-        for j in range(wi + 1, len(code)):
-            mnem, ops = code[j][1], code[j][2]
-            if mnem.startswith(("s_cbranch", "s_branch")):
-                tgt = re.search(r"<\S+\+0x([0-9a-f]+)>", ops)
-                base = code[0][0]
-                if tgt and base + int(tgt.group(1), 16) <= code[wi][0]:
-                    head = addr[base + int(tgt.group(1), 16)]
-                    body = code[head:j + 1]
-                    dma = sum(1 for _, m, o in body if _lds_dma(m, o))
-                    other = sum(1 for _, m, o in body if _vmem(m) and not _lds_dma(m, o))
-                    assert dma == ni and other == 0, f"{name}: loop issues {dma} DMA + {other} other loads"
-                    found += 1
-                    break
-    return found
+    wset = {w for w, _ in waits}
+
+    def walk(starts: list[int]) -> set[tuple[str, int, int]]:
+        """(end kind, DMA count, any other load) over every path from code[k], k in starts, to the next wait or the
+        end."""
+        ends, seen, todo = set(), set(), [(k, 0, 0) for k in starts]
+        while todo:
+            i, dma, other = todo.pop()
+            if (i, dma, other) in seen:
+                continue
+            seen.add((i, dma, other))
+            assert dma <= s * ni and len(seen) < 200000, f"{name}: a path from {starts} issues {dma} DMA loads"
+            if i in wset:
+                ends.add(("wait", dma, other))
+                continue
+            m, o = code[i][1], code[i][2]
+            dma2, other2 = dma + _lds_dma(m, o), min(1, other + (_vmem(m) and not _lds_dma(m, o)))
+            succ = _successors(code, addr, i)
+            if not succ:
+                ends.add(("end", dma2, other2))
+            todo.extend((k, dma2, other2) for k in succ)
+        return ends
+
+    first = walk([0])
+    assert {(k, d) for k, d, _ in first if k == "wait"} == {("wait", (s - 1) * ni)}, (name, first)
+    for w, _ in waits:
+        for kind, dma, other in walk(_successors(code, addr, w)):
+            assert dma == ni or (kind == "end" and dma == 0), \
+                f"{name}: a path from the wait at {w} to the next {kind} issues {dma} DMA loads"
+            assert kind == "end" or other == 0, f"{name}: a step issues {other} other loads"
+    return len(waits)
+
+
+def test_ring_step_check_rejects_a_planted_extra_load():
+    """The path walk on a hand-written two-stage loop (NI = 2, S = 3): accepted as written, rejected when one step
+    issues a third direct-to-LDS load or a register load, or when the wait count is off by one."""
+    def prog(extra: str = "", wait: int = 2) -> list[tuple[int, str, str]]:
+        body = [("buffer_load_dword", "v0, v1, s[0:3], 0 offen lds"), ("buffer_load_dword", "v0, v1, s[0:3], 0 offen lds")]
+        loop = [("s_waitcnt", f"vmcnt({wait}) lgkmcnt(0)"), ("s_barrier", "")] + body
+        if extra:
+            loop.append(("buffer_load_dword", extra))
+        loop += [("v_mfma_f32_16x16x32_bf16", "v[0:3], v[4:7], v[8:11], v[0:3]"), ("s_cbranch_scc1", "<k+0x{:x}>")]
+        code = body * 2 + loop + [("s_endpgm", "")]
+        out = []
+        for i, (m, o) in enumerate(code):
+            out.append((0x1000 + 4 * i, m, o.format(4 * 4) if m == "s_cbranch_scc1" else o))
+        return out
+
+    assert _check_ring_loops("ok", prog(), 2, 3) == 1
+    for bad in (prog("v0, v1, s[0:3], 0 offen lds"), prog("v2, v1, s[0:3], 0 offen"), prog(wait=3)):
+        with pytest.raises(AssertionError):
+            _check_ring_loops("bad", bad, 2, 3)
 
 
 def test_ring_kernel_loop_issues_one_slice_and_waits_for_the_next(kernels):
