@@ -40,6 +40,11 @@ hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int
 hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq,
                                 const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
                                 int64_t ldy, int M, int N, int K, int gs, hipStream_t s);
+bool w8a16_gemv_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt,
+                   int64_t lds, int64_t M, int64_t N, int64_t K, int gs, int64_t G);
+hipError_t launch_w8a16_gemv(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                             const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                             int64_t ldy, int M, int N, int K, int gs, bool single_group, int64_t G, hipStream_t s);
 bool w8_big_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int64_t K, int gs, int64_t G);
 hipError_t launch_w8_big(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq, const void* scales,
                          int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M,
@@ -558,7 +563,7 @@ size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
   // the prefill kernel's split-K partials, whenever it may run (its alignment conditions are checked at launch)
   const bool prefill_shape = (K % 64 == 0) && (gs % 32 == 0 || G == 1);
-  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA) return 0;
+  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return 0;
   return fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0);
 }
 
@@ -579,14 +584,26 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
   if (n_groups < G)
     return fail(FG_EINVAL, "fg_w8a16_gemm: n_groups=%d does not cover K=%lld with group %d", n_groups, (long long)K, gs);
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
-  if (impl != FG_W4_AUTO && impl != FG_W4_MFMA && impl != FG_W4_PREFILL && impl != FG_W4_GENERIC)
+  if (impl != FG_W4_AUTO && impl != FG_W4_GEMV && impl != FG_W4_MFMA && impl != FG_W4_PREFILL &&
+      impl != FG_W4_GENERIC)
     return fail(FG_EINVAL, "fg_w8a16_gemm: unknown impl %d", impl);
   const bool xbf16 = x_dtype == FG_BF16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool gemv = fg::w8a16_gemv_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);
   const bool big = fg::w8_big_ok(x, ldx, qweight, ldq, K, gs, G);
-  int kern = impl == FG_W4_GENERIC ? 0 : (impl == FG_W4_MFMA ? 1 : (impl == FG_W4_PREFILL ? 2 : -1));
-  if (kern < 0) kern = (skinny && M <= 64) ? 1 : (big ? 2 : 0);
+  int kern = impl == FG_W4_GENERIC ? 0
+             : impl == FG_W4_MFMA  ? 1
+             : impl == FG_W4_PREFILL ? 2
+             : impl == FG_W4_GEMV  ? 3
+                                   : -1;
+  // 1..2 rows: the decode GEMV (graph replays, M = 1, us, GEMV / skinny: qkv 6.2 / 9.6, o_proj 5.1 / 8.0, gate+up
+  // 20.7 / 28.7, down 12.6 / 17.3; M = 4 gate+up 34.4 / 27.7, so 3..64 rows stay on the skinny kernel)
+  if (kern < 0) kern = (gemv && M <= 2) ? 3 : ((skinny && M <= 64) ? 1 : (big ? 2 : 0));
+  if (kern == 3 && !gemv)
+    return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: decode GEMV needs M<=4, K%%16==0, group%%16==0 (or one group), "
+                                 "16-bit scales with lds%%8==0, ldq%%16==0, ldx%%8==0, 16-byte aligned x/qweight/"
+                                 "scales and N a multiple of its channels per wavefront");
   if (kern == 1 && !skinny)
     return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: skinny kernel needs M<=64, K%%128==0, group%%128==0 (or one group), "
                                  "16-bit scales, ldq%%16==0, ldx%%8==0 and 16-byte aligned x/qweight");
@@ -594,7 +611,10 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: prefill kernel needs K%%64==0, group%%32==0 (or one group), "
                                  "ldq%%16==0, ldx%%8==0 and 16-byte aligned x/qweight");
   hipError_t e;
-  if (kern == 1) {
+  if (kern == 3) {
+    e = fg::launch_w8a16_gemv(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy, (int)M,
+                              (int)N, (int)K, gs, G == 1, G, s);
+  } else if (kern == 1) {
     e = fg::launch_w8a16_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
                                 (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (kern == 2) {

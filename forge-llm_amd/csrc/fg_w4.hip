@@ -739,13 +739,7 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
   // 8-16 wavefronts otherwise.
   const int nblk = (N + r - 1) / r, cus = device_cus();
   int bw = nblk >= 8 * cus ? max_waves / ks : max(2, 8 / ks);
-  if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) {
-    bw = nblk / cus;
-  } else if (nblk % (2 * cus) == 0 && (nblk / (2 * cus)) * ks <= max_waves) {
-    // two workgroups per CU (gate+up, 3584 blocks: 512 workgroups of 14 wavefronts 12.70 us against 12.94 for 448
-    // of 16)
-    bw = nblk / (2 * cus);
-  }
+  if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) bw = nblk / cus;
   while (bw * ks > max_waves && bw > 1) --bw;
   *S = s; *R = r; *KS = ks; *BW = bw;
   return true;

@@ -14,6 +14,10 @@
 // The row sums of x come from one MFMA per k-step against all-ones (in the accumulator layout); each step lies in one
 // group (group size a multiple of 128, or one group), so after a step  acc += s[n, g] * (that expression).
 //
+// Decode GEMV (M <= 4): the W4 split GEMV's structure (16 weight bytes per lane and row, K slices summed in order
+// through LDS) with the bytes turned into floats and multiplied in fp32, where 15 of the skinny kernel's 16 MFMA rows
+// would be empty.
+//
 // Generic kernel: any shape, stride, alignment, group size and scale dtype; one wavefront per output channel and up
 // to 4 rows of x, lanes stride over K, fp32 products q * s * x in the oracle's order of dequantise-then-multiply.
 #include "fg_device.h"
@@ -202,6 +206,142 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------ decode GEMV (M <= 4)
+// The W4 split GEMV's structure for int8 weights: a wavefront owns R consecutive output channels and one K slice of at
+// most S 16-column chunks per lane (chunk c = slice start + lane + 64 i: 16 weight bytes of each row, 32 bytes of each
+// row of x); the KS slices of a channel block are the KS wavefronts of one workgroup, summed in slice order through LDS
+// at the end (no workspace, deterministic).  Per chunk a lane turns its 16 x values into fp32 once, with their sum, and
+// reuses them for all R channels: byte b of u = q ^ 0x80 = q + 128 becomes a float by v_cvt_f32_ubyte{b} and meets x
+// in an fma, so d = sum x u - 128 sum x = sum x q with every product exact in fp32; then acc += s[g(c), n] * d.  All
+// loads are raw buffer loads issued unconditionally in the order of first use (x, scales, weights); a chunk past the
+// slice reads past the operands' spans (0, no traffic) and adds exactly 0.
+struct W8GemvArgs {
+  int KC;         // 16-column chunks of K
+  int cps;        // chunks per K slice
+  int gs16;       // group size / 16, 0 for one group per row
+  uint32_t gmul;  // group of chunk c = umulhi(c, gmul) when gs16 > 1 (floor((2^32 - 1) / gs16) + 1)
+  uint32_t qbytes, xbytes, sbytes;
+};
+
+constexpr int w8a16_gemv_max_threads(int mt) { return mt == 4 ? 512 : 1024; }
+
+template <int MT, int S, int R, bool XBF16, bool SBF16>
+__global__ void __launch_bounds__(w8a16_gemv_max_threads(MT)) w8a16_gemv_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ qw, int64_t ldq,
+    const uint16_t* __restrict__ scales, int64_t lds, const void* __restrict__ bias, int bdt,
+    uint16_t* __restrict__ y, int64_t ldy, int M, int N, W8GemvArgs a) {
+  static_assert(R * MT == 4 || R * MT == 8 || R * MT == 16, "rows x batch must be 4, 8 or 16");
+  static_assert(R == 4 || R == 8, "4 or 8 channels per wavefront");
+  __shared__ float red[16][R * MT];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wb = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // channel block within the workgroup
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.y);         // K slice
+  const int BW = (int)(blockDim.x / kWave), KS = (int)blockDim.y;
+  const int n0 = (blockIdx.x * BW + wb) * R;
+  const int nr = min(n0, N - R);  // first channel read (blocks past the end re-read the last block)
+  const int c0 = ks * a.cps, c1 = min(c0 + a.cps, a.KC);
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc(qw, a.qbytes), rx = buf_rsrc(x, a.xbytes), rs = buf_rsrc(scales, a.sbytes);
+
+  uint32_t xo[S], wo[S], so[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int c = c0 + lane + kWave * i;
+    const bool ok = c < c1;
+    const uint32_t g = a.gs16 > 1 ? __umulhi((uint32_t)c, a.gmul) : (a.gs16 == 1 ? (uint32_t)c : 0u);
+    xo[i] = ok ? (uint32_t)c * 32u : a.xbytes;
+    wo[i] = ok ? (uint32_t)c * 16u : a.qbytes;
+    so[i] = ok ? g * (uint32_t)lds * 2u : a.sbytes;
+  }
+  uint4 xv[MT][S][2];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        xv[m][i][h] = buf_ld16(rx, xo[i] + 16u * h, (uint32_t)min(m, M - 1) * (uint32_t)ldx * 2u);
+  uint32_t sraw[S][R / 2];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if constexpr (R == 8) {
+      const uint4 t = buf_ld16(rs, so[i], (uint32_t)nr * 2u);
+      sraw[i][0] = t.x; sraw[i][1] = t.y; sraw[i][2] = t.z; sraw[i][3] = t.w;
+    } else {
+      const uint2 t = buf_ld8(rs, so[i], (uint32_t)nr * 2u);
+      sraw[i][0] = t.x; sraw[i][1] = t.y;
+    }
+  }
+  uint4 wv[R][S];
+  const uint32_t ldqb = (uint32_t)ldq;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < S; ++i) wv[r][i] = buf_ld16_nt(rq, wo[i], ((uint32_t)nr + (uint32_t)r) * ldqb);
+
+  float acc[R * MT];
+#pragma unroll
+  for (int v = 0; v < R * MT; ++v) acc[v] = 0.f;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    float xf[MT][16], xs[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint32_t wd[8] = {xv[m][i][0].x, xv[m][i][0].y, xv[m][i][0].z, xv[m][i][0].w,
+                              xv[m][i][1].x, xv[m][i][1].y, xv[m][i][1].z, xv[m][i][1].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xf[m][2 * e] = XBF16 ? __uint_as_float(wd[e] << 16) : f16_bits_to_f32((uint16_t)wd[e]);
+        xf[m][2 * e + 1] = XBF16 ? __uint_as_float(wd[e] & 0xffff0000u) : f16_bits_to_f32((uint16_t)(wd[e] >> 16));
+        sum += xf[m][2 * e];
+        sum += xf[m][2 * e + 1];
+      }
+      xs[m] = sum;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t sb = (r & 1) ? sraw[i][r >> 1] >> 16 : sraw[i][r >> 1] & 0xffffu;
+      const float sc = SBF16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32((uint16_t)sb);
+      float d[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) d[m] = -128.f * xs[m];
+      const uint32_t wq[4] = {wv[r][i].x, wv[r][i].y, wv[r][i].z, wv[r][i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t u = wq[q] ^ 0x80808080u;  // q + 128 per byte
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float fu = (float)((u >> (8 * b)) & 0xffu);
+#pragma unroll
+          for (int m = 0; m < MT; ++m) d[m] = __builtin_fmaf(xf[m][4 * q + b], fu, d[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r * MT + m] = __builtin_fmaf(sc, d[m], acc[r * MT + m]);
+    }
+  }
+  const float tot = wave_transpose_sum<R * MT>(acc, lane);
+  constexpr int span = kWave / (R * MT);
+  auto store = [&](int idx, float v) {
+    const int r = idx / MT, m = idx - (idx / MT) * MT;
+    if (m < M && n0 + r < N) {
+      if (bias) v += load_f(bias, bdt, n0 + r);
+      y[(int64_t)m * ldy + n0 + r] = XBF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+    }
+  };
+  if (KS == 1) {
+    if ((lane % span) == 0) store(lane / span, tot);
+  } else {
+    if ((lane % span) == 0) red[ks * BW + wb][lane / span] = tot;
+    __syncthreads();
+    if (ks == 0 && lane < R * MT) {  // the K slices of this block, summed in slice order
+      float v = 0.f;
+      for (int k2 = 0; k2 < KS; ++k2) v += red[k2 * BW + wb][lane];
+      store(lane, v);
+    }
+  }
+}
+
 // Generic: one wavefront per (channel n, up to 4 rows of x); fixed-order lane and cross-lane sums.
 __global__ void __launch_bounds__(256) w8a16_generic_kernel(const void* __restrict__ x, int64_t ldx, int xdt,
                                                             const int8_t* __restrict__ qw, int64_t ldq,
@@ -303,6 +443,90 @@ hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int
   }
   if (sbf) return launch_w8a16_skinny_x<false, true>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
   return launch_w8a16_skinny_x<false, false>(mb, T, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gsteps, KS, BW, s);
+}
+
+// Decode GEMV launch shape: R = 8 channels per wavefront (4 for four rows of x); S = 1 chunk per lane while K <= 4096
+// (KS = 4 slices of 1024 columns), else 4 (2 with four rows of x); one channel block per workgroup, i.e. a workgroup is
+// the KS wavefronts of one block.  Graph replays over a 1.2 GB ring, M = 1, us (this shape / 16-wavefront workgroups):
+// gate+up 19.2 / 23.9 (6.1 TB/s), down (S = 4, 4 slices) 11.6 / 11.9, o_proj 4.9 / 5.6, qkv 6.1 / 6.5: small
+// workgroups retire and refill independently.
+struct W8GemvPlan {
+  int mt, S, R, KS, BW;
+};
+static bool w8a16_gemv_plan(int M, int N, int K, W8GemvPlan* p) {
+  const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  const int KC = K / 16, R = mt == 4 ? 4 : 8;
+  const int S = KC <= 4 * kWave ? 1 : (mt == 4 ? 2 : 4);
+  const int ks = (KC + kWave * S - 1) / (kWave * S);
+  const int maxw = w8a16_gemv_max_threads(mt) / kWave;
+  if (ks > maxw || N % R != 0) return false;
+  *p = W8GemvPlan{mt, S, R, ks, 1};
+  return true;
+}
+
+bool w8a16_gemv_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt,
+                   int64_t lds, int64_t M, int64_t N, int64_t K, int gs, int64_t G) {
+  const int64_t k4g = 1LL << 32;
+  W8GemvPlan p;
+  return M > 0 && M <= 4 && sdt != FG_F32 && (K % 16) == 0 && ((gs % 16) == 0 || G == 1) && (ldx % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 &&
+         (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 8) == 0 &&
+         (reinterpret_cast<uintptr_t>(scales) % 16) == 0 && N * ldq < k4g && M * ldx * 2 < k4g &&
+         G * lds * 2 < k4g && K < k4g / 32 && w8a16_gemv_plan((int)M, (int)N, (int)K, &p);
+}
+
+template <int MT, int S, int R, bool XBF16, bool SBF16>
+static hipError_t launch_w8a16_gemv_t(const W8GemvPlan& p, const void* x, int64_t ldx, const int8_t* qw, int64_t ldq,
+                                      const void* scales, int64_t lds, const void* bias, int bdt, void* y,
+                                      int64_t ldy, int M, int N, int K, int gs16, int64_t G, hipStream_t s) {
+  W8GemvArgs a;
+  a.KC = K / 16;
+  a.cps = (a.KC + p.KS - 1) / p.KS;
+  a.gs16 = gs16;
+  a.gmul = gs16 > 1 ? 0xffffffffu / (uint32_t)gs16 + 1u : 0u;
+  a.qbytes = (uint32_t)((int64_t)N * ldq);
+  a.xbytes = (uint32_t)((int64_t)M * ldx * 2);
+  a.sbytes = (uint32_t)(G * lds * 2);
+  const int nblk = N / R;
+  hipLaunchKernelGGL((w8a16_gemv_kernel<MT, S, R, XBF16, SBF16>), dim3((nblk + p.BW - 1) / p.BW),
+                     dim3(kWave * p.BW, p.KS), 0, s, static_cast<const uint16_t*>(x), ldx, qw, ldq,
+                     static_cast<const uint16_t*>(scales), lds, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, a);
+  return hipGetLastError();
+}
+
+template <bool XBF16, bool SBF16>
+static hipError_t launch_w8a16_gemv_x(const W8GemvPlan& p, const void* x, int64_t ldx, const int8_t* qw, int64_t ldq,
+                                      const void* scales, int64_t lds, const void* bias, int bdt, void* y,
+                                      int64_t ldy, int M, int N, int K, int gs16, int64_t G, hipStream_t s) {
+#define FG_W8G(MT_, S_, R_)                                                                                       \
+  return launch_w8a16_gemv_t<MT_, S_, R_, XBF16, SBF16>(p, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, \
+                                                        K, gs16, G, s)
+  if (p.mt == 1) {
+    if (p.S == 4) FG_W8G(1, 4, 8);
+    FG_W8G(1, 1, 8);
+  }
+  if (p.mt == 2) {
+    if (p.S == 4) FG_W8G(2, 4, 8);
+    FG_W8G(2, 1, 8);
+  }
+  if (p.S == 2) FG_W8G(4, 2, 4);
+  FG_W8G(4, 1, 4);
+#undef FG_W8G
+}
+
+hipError_t launch_w8a16_gemv(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                             const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
+                             int64_t ldy, int M, int N, int K, int gs, bool single_group, int64_t G, hipStream_t s) {
+  W8GemvPlan p;
+  if (!w8a16_gemv_plan(M, N, K, &p)) return hipErrorInvalidValue;
+  const int gs16 = single_group ? 0 : gs / 16;
+  const bool sbf = sdt == FG_BF16;
+  if (xbf16) {
+    if (sbf) return launch_w8a16_gemv_x<true, true>(p, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gs16, G, s);
+    return launch_w8a16_gemv_x<true, false>(p, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gs16, G, s);
+  }
+  if (sbf) return launch_w8a16_gemv_x<false, true>(p, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gs16, G, s);
+  return launch_w8a16_gemv_x<false, false>(p, x, ldx, qw, ldq, scales, lds, bias, bdt, y, ldy, M, N, K, gs16, G, s);
 }
 
 hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq,

@@ -1,4 +1,5 @@
-"""GPU parity of W8A16 (fg_w8a16_gemm through the C ABI: skinny MFMA, dequantise-to-LDS prefill and generic kernels)
+"""GPU parity of W8A16 (fg_w8a16_gemm through the C ABI: decode GEMV, skinny MFMA, dequantise-to-LDS prefill and generic
+kernels)
 against the CPU oracle (forge/kernels/ref/gemm_w4a16.py:45-52 restated in oracle/gemm.py).  Bar: max|y - ref| /
 max|ref| <= 1e-2 of the fp32 oracle and the reference's compare() rule for bf16 / fp16 outputs."""
 from __future__ import annotations
@@ -44,6 +45,51 @@ def test_skinny_matches_oracle(m, n, k, gs, xdt):
     sdt = torch.bfloat16 if m % 2 else torch.float16
     y, ref = _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n, config={"impl": "mfma"})
     assert_close(y.cpu(), ref, ODT[xdt], what=f"w8a16 skinny m={m} n={n} k={k} gs={gs}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k,gs", [(4096, 4096, -1), (776, 2048, 128), (1032, 1024, 256), (512, 960, 48),
+                                    (264, 20480, 128), (8, 16, 16)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_gemv_matches_oracle(m, n, k, gs, xdt):
+    """The split-K decode GEMV forced (one, two and four chunks per lane, group sizes that are not powers of two, a K
+    of one chunk), against the oracle; for one or two rows the policy takes it too and gives the same bits."""
+    sdt = torch.bfloat16 if (m + n) % 2 else torch.float16
+    if m > 2 and k > 16384:  # four rows of x: at most 8 slices of 1024 columns; the policy takes the skinny kernel
+        with pytest.raises(ForgeError):
+            _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n + k, config={"impl": "gemv"})
+        y2, ref = _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n + k)
+        assert_close(y2.cpu(), ref, ODT[xdt], what=f"w8a16 policy m={m} n={n} k={k} gs={gs}")
+        return
+    y, ref = _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n + k, config={"impl": "gemv"})
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"w8a16 gemv m={m} n={n} k={k} gs={gs}")
+    y2, _ = _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n + k)
+    if m <= 2:  # the policy's own choice for one or two rows
+        assert torch.equal(y, y2), f"gemv m={m} n={n}: policy differs from the forced GEMV"
+    else:
+        assert_close(y2.cpu(), ref, ODT[xdt], what=f"w8a16 policy m={m} n={n} k={k} gs={gs}")
+
+
+def test_gemv_extremes_and_rejects():
+    """Weights at -128 and 127 with large x (exact products, fp32 sums), NaN / inf in x propagate, run-to-run bits;
+    the forced GEMV rejects 5 rows and channel counts that its wavefronts do not divide."""
+    n, k = 1024, 4096
+    q = torch.full((n, k), 127, dtype=torch.int8)
+    q[::2] = -128
+    s = torch.full((n, 1), 0.5, dtype=torch.float16)
+    p = L.pack_w8(q, s, -1).to(DEV)
+    x = (torch.randn(2, k, generator=gen(81)) * 100).bfloat16()
+    x[1, 7] = float("nan")
+    y = ops.w8a16_linear(x.to(DEV), p, config={"impl": "gemv"})
+    ref = og.w8a16_gemm_ref(to_f32(x[:1]), og.pack_w8(q.numpy(), s.float().numpy(), -1))
+    assert_close(y[:1].cpu(), ref, "bfloat16", what="gemv extremes")
+    assert torch.isnan(y[1].float()).all()
+    assert all(torch.equal(y[:1], ops.w8a16_linear(x.to(DEV), p, config={"impl": "gemv"})[:1]) for _ in range(3))
+    with pytest.raises(ForgeError):
+        ops.w8a16_linear(x_act(5, k, seed=82).to(DEV), p, config={"impl": "gemv"})
+    q2, s2 = _w8(100, 256, -1, seed=83)
+    with pytest.raises(ForgeError):
+        ops.w8a16_linear(x_act(1, 256, seed=84).to(DEV), L.pack_w8(q2, s2, -1).to(DEV), config={"impl": "gemv"})
 
 
 @pytest.mark.parametrize("m,n,k,gs", [(65, 256, 512, 32), (128, 777, 1024, -1), (300, 2048, 2048, 128)])
