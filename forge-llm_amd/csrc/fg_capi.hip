@@ -68,6 +68,12 @@ hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t*
 bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
                 int64_t lds, const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
 bool w4_ring_preferred(bool portable, int M, int N, int K);
+size_t w4_libgemm_workspace_bytes(int N, int K);
+bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t K);
+hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
+                             int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
+                             const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
+                             void* ws, size_t ws_bytes, hipStream_t s);
 size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K);
 hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
                           const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias,
@@ -229,6 +235,12 @@ namespace {
 // kernel: measured on the Llama-3-8B shapes, the skinny kernel wins up to 32 rows (and to 64 rows for N, K <= 4096),
 // the prefill kernel from 48 rows (gate+up at M = 64: 1.10 against 0.60 TB/s).
 constexpr int64_t kPrefillMinM = 33;
+// Rows from which the policy takes the dequantise + library GEMM route (when the caller's workspace can hold it): the
+// dequantisation costs 2.5 N K bytes once, the fused kernel loses a share of every MFMA cycle.  Graph replays over four
+// distinct weights, us, fused / dequantise + GEMM: M = 1024 qkv 87.9 / 72.9, o_proj 65.0 / 56.8, down 177 / 172,
+// gate+up 261 / 278; M = 2048 127 / 104, 93 / 77, 297 / 248, 494 / 438; M = 8192 408 / 310, 282 / 203, 844 / 645,
+// 1711 / 1302; M = 512 fused ahead (down 97 / 133).
+int64_t dequant_gemm_min_m(int64_t N, int64_t K) { return N * K > (64LL << 20) ? 1536 : 1024; }
 
 // Whether the automatic policy sends a 9..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
 // 13..16 over N >= 16384 and 9..12 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
@@ -247,10 +259,11 @@ struct W4Plan {
   int gemv, mt, rows, max_blocks;  // GEMV: FG_GEMV_* kernel, rows of x per pass, wave-kernel knobs
   int tile_m, splits;              // MFMA
   size_t ws_bytes;
+  bool dequant_gemm;  // AUTO with many rows: the launch takes the dequantise + library GEMM route where it applies
 };
 
 int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned, bool q_aligned, bool has_g_idx,
-            const fg_w4_config* cfg, W4Plan* p) {
+            const fg_w4_config* cfg, bool allow_dequant_gemm, W4Plan* p) {
   const int gs = group_size > 0 ? group_size : (int)K;
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
   const int G = (int)((K + gs - 1) / gs);
@@ -283,9 +296,24 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
   if (use == FG_W4_MFMA && !mfma_ok)
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: MFMA path needs no g_idx, K%%8==0, ldq%%4==0, ldx%%8==0 and "
                                  "16-byte aligned x/qweight");
-  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC && use != FG_W4_PREFILL)
+  if (use == FG_W4_DEQUANT_GEMM && !allow_dequant_gemm)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_noalloc: the dequantise + library GEMM route needs a caller workspace");
+  if (use == FG_W4_DEQUANT_GEMM && K % 8 != 0)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs K %% 8 == 0");
+  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC && use != FG_W4_PREFILL &&
+      use != FG_W4_DEQUANT_GEMM)
     return fail(FG_EINVAL, "fg_w4a16_gemm: unknown impl %d", impl);
-  *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0};
+  *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0, false};
+  // many rows under the policy: the launch takes the dequantise + library GEMM route if the operands allow it (16-bit
+  // x, the bias type, no perm), else the kernel chosen above; the workspace covers both
+  const bool dq_auto = impl == FG_W4_AUTO && allow_dequant_gemm && M >= dequant_gemm_min_m(N, K) && K % 8 == 0 &&
+                       (use == FG_W4_PREFILL || use == FG_W4_MFMA || use == FG_W4_GENERIC) &&
+                       !(cfg && (cfg->tile_m || cfg->split_k));
+  if (use == FG_W4_DEQUANT_GEMM || dq_auto) {
+    p->dequant_gemm = true;
+    p->ws_bytes = fg::w4_libgemm_workspace_bytes((int)N, (int)K);
+    if (use == FG_W4_DEQUANT_GEMM) return FG_OK;
+  }
   if (use == FG_W4_GEMV) {
     p->rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 4;
     if (p->rows != 1 && p->rows != 2 && p->rows != 4) return fail(FG_EINVAL, "fg_w4a16_gemm: rows_per_wave must be 1, 2 or 4");
@@ -295,7 +323,8 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
     int kchunk = 0, used = 1;
     fg::w4_mfma_split_plan((int)M, (int)N, (int)K, p->tile_m, cfg ? cfg->split_k : 0, &kchunk, &used);
     p->splits = cfg && cfg->split_k ? cfg->split_k : 0;
-    p->ws_bytes = used > 1 ? (size_t)used * (size_t)M * (size_t)N * sizeof(float) : 0;
+    const size_t wm = used > 1 ? (size_t)used * (size_t)M * (size_t)N * sizeof(float) : 0;
+    if (wm > p->ws_bytes) p->ws_bytes = wm;
     // the launch picks among the skinny, prefill and tiled MFMA kernels once the operand addresses are known (an
     // act-order perm or misaligned operands rule some out): size the workspace for either split-K kernel
     if (prefill_ok) {
@@ -319,7 +348,7 @@ size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
                                 int32_t q_aligned, int32_t has_g_idx, const fg_w4_config* cfg) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
   W4Plan p;
-  if (plan_w4(M, N, K, group_size, x_aligned != 0, q_aligned != 0, has_g_idx != 0, cfg, &p) != FG_OK) return 0;
+  if (plan_w4(M, N, K, group_size, x_aligned != 0, q_aligned != 0, has_g_idx != 0, cfg, true, &p) != FG_OK) return 0;
   return p.ws_bytes;
 }
 
@@ -354,7 +383,7 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   const bool x_aligned = (ldx % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
   const bool q_aligned = (ldq % 4 == 0) && (reinterpret_cast<uintptr_t>(qweight) % 16 == 0);
   W4Plan p;
-  const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, &p);
+  const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, !static_ws, &p);
   if (rc != FG_OK) return rc;
   if (static_ws && p.ws_bytes > workspace_bytes)
     return fail(FG_EINVAL, "fg_w4a16_gemm_noalloc: this launch needs %zu bytes of split-K scratch, the library's static "
@@ -367,6 +396,18 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
+  if (p.dequant_gemm) {
+    const bool fits = perm == nullptr && fg::w4_libgemm_ok(x_dtype, bias, bias_dtype, K) &&
+                      reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
+    if (fits)
+      return hip_status(fg::launch_w4_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
+                                              g_idx, bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, workspace,
+                                              workspace_bytes, s),
+                        "fg_w4a16_gemm dequantise + library GEMM");
+    if (p.impl == FG_W4_DEQUANT_GEMM)
+      return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs no act-order perm, a bias "
+                                   "in fp32 or x's dtype and a 256-byte aligned workspace");
+  }
   // 3-4 rows over weights larger than 4096 x 4096: the skinny MFMA kernel where it applies (it needs no workspace).
   // Measured at M = 4 (us): qkv 8.2 against 8.7 for the GEMV, gate+up 20.5 against 22.8, down 14.8 against 16.2;
   // o_proj (4096 x 4096) 6.8 against 6.1 stays on the GEMV, as do 1-2 rows.

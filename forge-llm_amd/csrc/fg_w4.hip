@@ -894,6 +894,42 @@ __global__ void __launch_bounds__(256) w4_dequant_kernel(
   }
 }
 
+// Dense dequantisation to a 16-bit output, one thread per 32 columns of one row (16 bytes of qweight in, 64 bytes
+// out, every access a 16-byte vector): (q - z) * s = fma(q, s, -z * s), exact in fp32 (both products and their sum
+// are exact for |q - z| <= 15 and a 16-bit scale), rounded once to nearest even -- the generic kernel's value, bit
+// for bit.  Needs K % 32 == 0, groups of whole 32-column chunks (or one group), 16-bit scales, no g_idx, 16-byte
+// aligned qweight / out with ldq % 4 == 0 and ldo % 8 == 0.
+template <bool OBF16>
+__global__ void __launch_bounds__(256) w4_dequant16_kernel(const int32_t* __restrict__ qw, int64_t ldq,
+                                                           const uint16_t* __restrict__ scales, int sbf16, int64_t lds,
+                                                           const int32_t* __restrict__ zeros, int64_t ldz,
+                                                           uint16_t* __restrict__ out, int64_t ldo, int N, int KC,
+                                                           int gs32) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)N * KC) return;
+  const int n = (int)(t / KC), c = (int)(t - (int64_t)n * KC);
+  const int g = gs32 > 0 ? c / gs32 : 0;
+  const uint4 w = load16_stream(qw + (int64_t)n * ldq + 4 * c);
+  const uint16_t sb = scales[(int64_t)g * lds + n];
+  const float sc = sbf16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
+  const float z = zeros ? (float)nibble((uint32_t)zeros[(int64_t)g * ldz + n / 8], n & 7) : 8.f;
+  const float cz = -z * sc;
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  uint4* o = reinterpret_cast<uint4*>(out + (int64_t)n * ldo + 32 * c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = __builtin_fmaf((float)nibble(wd[i], 2 * j), sc, cz);
+      const float hi = __builtin_fmaf((float)nibble(wd[i], 2 * j + 1), sc, cz);
+      h[j] = OBF16 ? (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16)
+                   : (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    }
+    o[i] = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 size_t w4_gemv_lds_bytes(int mt, int K) {
   const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
@@ -1054,6 +1090,18 @@ hipError_t launch_w4_generic(const void* x, int64_t ldx, int xdt, const int32_t*
 hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
                              const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int odt, int64_t ldo,
                              int N, int K, int gs, hipStream_t s) {
+  const bool one_group = gs >= K;
+  if (!g_idx && (odt == FG_BF16 || odt == FG_F16) && (sdt == FG_BF16 || sdt == FG_F16) && K % 32 == 0 &&
+      (gs % 32 == 0 || one_group) && ldq % 4 == 0 && reinterpret_cast<uintptr_t>(qw) % 16 == 0 && ldo % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    const int KC = K / 32;
+    const int64_t blocks = ((int64_t)N * KC + 255) / 256;
+    auto kern = odt == FG_BF16 ? w4_dequant16_kernel<true> : w4_dequant16_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, static_cast<const uint16_t*>(scales),
+                       (int)(sdt == FG_BF16), lds, zeros, ldz, static_cast<uint16_t*>(out), ldo, N, KC,
+                       one_group ? 0 : gs / 32);
+    return hipGetLastError();
+  }
   const int64_t total = (int64_t)N * ((K + 7) / 8);
   const int64_t blocks = (total + 255) / 256;
   hipLaunchKernelGGL(w4_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, scales, sdt, lds, zeros, ldz,

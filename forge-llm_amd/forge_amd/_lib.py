@@ -22,9 +22,9 @@ W4A16_SCRATCH_BYTES = 64 << 20  # FG_W4A16_SCRATCH_BYTES
 # status codes
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 # W4A16 impl codes
-W4_AUTO, W4_GEMV, W4_MFMA, W4_GENERIC, W4_PREFILL = 0, 1, 2, 3, 4
+W4_AUTO, W4_GEMV, W4_MFMA, W4_GENERIC, W4_PREFILL, W4_DEQUANT_GEMM = 0, 1, 2, 3, 4, 5
 W4_IMPL = {None: W4_AUTO, "auto": W4_AUTO, "gemv": W4_GEMV, "mfma": W4_MFMA, "generic": W4_GENERIC,
-           "prefill": W4_PREFILL}
+           "prefill": W4_PREFILL, "dequant_gemm": W4_DEQUANT_GEMM}
 GEMV_AUTO, GEMV_SPLIT, GEMV_TILE, GEMV_WAVE = 0, 1, 2, 3
 GEMV_KERNEL = {None: GEMV_AUTO, "auto": GEMV_AUTO, "split": GEMV_SPLIT, "tile": GEMV_TILE, "wave": GEMV_WAVE}
 

@@ -4,7 +4,7 @@ Recipe (also what ``python -m forge_amd.build`` runs)::
 
     hipcc --offload-arch=gfx950 -O3 -std=c++17 -fPIC -ffp-contract=off \
           -Xclang -target-feature -Xclang -packed-fp32-ops -c csrc/<file>.hip -o _build/<file>.o   (each file, in parallel)
-    hipcc --offload-arch=gfx950 -shared -o forge_amd/libforge_mi355x.so _build/*.o
+    hipcc --offload-arch=gfx950 -shared -o forge_amd/libforge_mi355x.so _build/*.o -L/opt/rocm/lib -lhipblaslt
 
 ``-ffp-contract=off`` keeps every fp32 multiply and add separately rounded unless the source asks for an fma, so
 epilogues such as ``(float(acc) * sa) * sb + bias`` round exactly like the CPU oracle.  Packed fp32 instructions are
@@ -27,6 +27,8 @@ ARCH = os.environ.get("FORGE_AMD_ARCH", "gfx950")
 
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# hipBLASLt serves the plain bf16 / fp16 GEMM of the dequantise + library GEMM route (fg_libgemm.hip)
+LINK = ["-L" + os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib"), "-lhipblaslt"]
 
 
 def _hipcc() -> str:
@@ -59,7 +61,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
     tmp = LIB + f".tmp{os.getpid()}"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs, *LINK]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True, capture_output=not verbose)

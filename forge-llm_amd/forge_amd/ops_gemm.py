@@ -247,13 +247,14 @@ def _selftest_fp8(dev: torch.device) -> bool:
 
 
 # ================================================================================================ W4A16
-_W4_IMPLS = {"gemv": "gemv", "dot": "mfma", "mfma": "mfma", "dequant_matmul": "mfma", "prefill": "prefill",
-             "legacy": "generic", "generic": "generic", "auto": None, None: None}
+_W4_IMPLS = {"gemv": "gemv", "dot": "mfma", "mfma": "mfma", "dequant_matmul": "dequant_gemm",
+             "dequant_gemm": "dequant_gemm", "prefill": "prefill", "legacy": "generic", "generic": "generic",
+             "auto": None, None: None}
 
 
 def forced_impl() -> str | None:
-    """``FORGE_W4_IMPL`` = gemv | mfma | prefill | generic (the reference's dot / dequant_matmul / legacy map to
-    mfma / mfma / generic); anything else means the policy."""
+    """``FORGE_W4_IMPL`` = gemv | mfma | prefill | dequant_gemm | generic (the reference's dot / dequant_matmul / legacy
+    map to mfma / dequant_gemm / generic); anything else means the policy."""
     return _W4_IMPLS.get(os.environ.get("FORGE_W4_IMPL", "").strip().lower())
 
 

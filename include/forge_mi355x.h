@@ -34,9 +34,14 @@ enum {
 enum { FG_OK = 0, FG_EINVAL = 1, FG_EUNSUPPORTED = 2, FG_EHIP = 3 };
 
 /* W4A16 implementation selector (fg_w4_config.impl) */
-enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_PREFILL = 4 };
+enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_PREFILL = 4, FG_W4_DEQUANT_GEMM = 5 };
 /* FG_W4_PREFILL: 128/256 x 256 tiles, x straight to LDS, weights dequantised to LDS (large M x N; needs K % 64 == 0,
-   group % 32 == 0 or one group, aligned x / qweight, no act-order perm) */
+   group % 32 == 0 or one group, aligned x / qweight, no act-order perm)
+   FG_W4_DEQUANT_GEMM: the reference's large-M route (forge/kernels/triton/gemm_w4_dequant.py:194-256): the weights
+   dequantised once into the workspace, then hipBLASLt's bf16 / fp16 GEMM (fp32 accumulation, bias in its epilogue);
+   the policy takes it from 1024 rows (1536 over weights above 64 Mi elements) when the caller's workspace holds it
+   (never in fg_w4a16_gemm_noalloc).  Needs
+   K % 8 == 0, no act-order perm (a g_idx is fine), a bias in fp32 or x's dtype, a 256-byte aligned workspace. */
 
 /* GEMV kernel selector (fg_w4_config.gemv_kernel) */
 enum { FG_GEMV_AUTO = 0, FG_GEMV_SPLIT = 1, FG_GEMV_TILE = 2, FG_GEMV_WAVE = 3 };

@@ -6,6 +6,7 @@ import pytest
 import torch
 import torch.nn as nn
 
+from forge_amd import _lib
 from forge_amd import layouts as L
 from forge_amd import ops_gemm as ops
 from forge_amd.errors import ConfigError, HardwareUnsupported
@@ -79,7 +80,9 @@ def test_w4_config_aliases(monkeypatch):
     with pytest.raises(ConfigError):
         ops._w4_config({"impl": "bogus"})
     monkeypatch.setenv("FORGE_W4_IMPL", "dequant_matmul")
-    assert ops._w4_config(None).impl == 2
+    assert ops._w4_config(None).impl == _lib.W4_DEQUANT_GEMM
+    monkeypatch.setenv("FORGE_W4_IMPL", "dot")
+    assert ops._w4_config(None).impl == _lib.W4_MFMA
 
 
 def test_packed_linear_modules_keep_reference_buffer_names():
