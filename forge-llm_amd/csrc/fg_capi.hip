@@ -68,6 +68,10 @@ hipError_t launch_w4_frag(const void* x, int64_t ldx, bool xbf16, const int32_t*
 bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
                 int64_t lds, const int32_t* zeros, int64_t ldz, int M, int64_t N, int64_t K, int gs, int64_t G);
 bool w4_ring_preferred(bool portable, int M, int N, int K);
+bool int8_gemv_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N, int64_t K);
+hipError_t launch_int8_gemv(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
+                            int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
+                            int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
 size_t w4_libgemm_workspace_bytes(int N, int K);
 bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t K);
 hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
@@ -690,6 +694,15 @@ int fg_int8_gemm(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, 
   if (lda < K || ldb < K || ldy < N) return fail(FG_EINVAL, "fg_int8_gemm: leading dimensions too small");
   if (y_dtype == FG_I32 && bias)
     return fail(FG_EINVAL, "fg_int8_gemm: a bias cannot be added to the raw int32 accumulator (y_dtype FG_I32)");
+  // 1..2 rows of A: the decode GEMV (tile_m = 1 forces it)
+  const bool gemv = fg::int8_gemv_ok(a, lda, b, ldb, M, N, K);
+  if (cfg && cfg->tile_m == 1 && !gemv)
+    return fail(FG_EUNSUPPORTED, "fg_int8_gemm: tile_m=1 (decode GEMV) needs M <= 2, K %% 16 == 0, N %% 8 == 0 and "
+                                 "16-byte aligned operands with leading dimensions that are multiples of 16");
+  if (gemv && ((cfg && cfg->tile_m == 1) || (!(cfg && cfg->tile_m) && M <= 2)))
+    return hip_status(fg::launch_int8_gemv(a, lda, sa, sa_len, b, ldb, sb, sb_len, bias, bias_dtype, y, ldy, y_dtype,
+                                           (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream)),
+                      "fg_int8_gemm launch");
   bool ring;
   const int tile = mm_tile(M, N, K, true, a, lda, b, ldb, cfg, &ring);
   if (tile == -2) return fail(FG_EINVAL, "fg_int8_gemm: tile_m must be 0, 16, 64, 128 or 256, got %d", cfg->tile_m);

@@ -147,6 +147,52 @@ __device__ __forceinline__ float wave_transpose_sum(float (&v)[V], int lane) {
   return cur[0];
 }
 
+// wave_transpose_sum for int32 partials (exact integer adds; the lane moves are the same bit moves).
+template <int V>
+__device__ __forceinline__ int wave_transpose_sum_i32(int (&v)[V], int lane) {
+  static_assert(V == 4 || V == 8 || V == 16, "V");
+  int cur[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) cur[i] = v[i];
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) {
+    float a = __builtin_bit_cast(float, cur[i]), b = __builtin_bit_cast(float, cur[i + V / 2]);
+    permlane32_swap(a, b);
+    cur[i] = __builtin_bit_cast(int, a) + __builtin_bit_cast(int, b);
+  }
+#pragma unroll
+  for (int i = 0; i < V / 4; ++i) {
+    float a = __builtin_bit_cast(float, cur[i]), b = __builtin_bit_cast(float, cur[i + V / 4]);
+    permlane16_swap(a, b);
+    cur[i] = __builtin_bit_cast(int, a) + __builtin_bit_cast(int, b);
+  }
+  auto partner = [&](auto o_tag, int v) {
+    constexpr int O = decltype(o_tag)::value;
+    return __builtin_bit_cast(int, dpp_partner<O>(__builtin_bit_cast(float, v)));
+  };
+  auto step = [&](auto o_tag, int n) {
+    constexpr int O = decltype(o_tag)::value;
+    const bool up = (lane & O) != 0;
+    if (n > 1) {
+#pragma unroll
+      for (int i = 0; i < V / 8; ++i) {
+        if (i < n / 2) {
+          const int send = up ? cur[i] : cur[i + n / 2];
+          const int keep = up ? cur[i + n / 2] : cur[i];
+          cur[i] = keep + partner(o_tag, send);
+        }
+      }
+    } else {
+      cur[0] += partner(o_tag, cur[0]);
+    }
+  };
+  step(std::integral_constant<int, 8>{}, V / 4);
+  step(std::integral_constant<int, 4>{}, V / 8 > 0 ? V / 8 : 1);
+  step(std::integral_constant<int, 2>{}, V / 16 > 0 ? V / 16 : 1);
+  step(std::integral_constant<int, 1>{}, 1);
+  return cur[0];
+}
+
 // Map a linear workgroup id to an output tile: first deal consecutive logical tiles to one XCD, then walk tiles in
 // groups of `gm` tile-rows so neighbouring workgroups share B (weight) slices and A (activation) slices.
 __device__ __forceinline__ void tile_of(int bid, int ntm, int ntn, int& tm, int& tn) {

@@ -67,7 +67,9 @@ typedef struct fg_mm_config {
                      width from tile_n or the policy), otherwise square register-staged tiles; 256 = the 256-row
                      direct-to-LDS kernel (256 x 256 tiles, 256 x 320 for INT8 with 16-bit outputs where that fills
                      the CUs' last round better) (needs the same K and alignment, else FG_EUNSUPPORTED); 16 = the
-                     skinny split-K kernel (M <= 64, K % 256 == 0, same alignment; modes 0 / 1) */
+                     skinny split-K kernel (M <= 64, K % 256 == 0, same alignment; modes 0 / 1); 1 = the INT8
+                     decode GEMV (fg_int8_gemm only: M <= 2, K % 16 == 0, N % 8 == 0, same alignment), which the policy
+                     takes for 1..2 rows */
   int32_t tile_n; /* ring kernel tile width: 32, 64 or 128 with tile_m = 64, 128 with tile_m = 128 (needs the ring
                      kernel's conditions, else FG_EUNSUPPORTED); 0 = policy; ignored for tile_m 16 / 256 */
   int32_t reserved[6];

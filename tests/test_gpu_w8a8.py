@@ -39,6 +39,42 @@ def test_int8_gemm_exact(m, n, k):
     assert np.array_equal(y, og.int8_gemm_ref(xq, sx, wq, sw, b.numpy(), acc=ref_acc))
 
 
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (776, 1008), (1024, 16), (264, 28672), (8, 8192)])
+def test_int8_gemv_exact(m, n, k):
+    """The decode GEMV (the policy's choice for 1..2 rows, and forced with tile_m=1): int32 accumulator and fp32 /
+    bf16 epilogue bit-exact against the oracle, with and without bias."""
+    xq, sx, wq, sw = _int8_operands(m, n, k, seed=m + n + k)
+    a, w = torch.from_numpy(xq).to(DEV), torch.from_numpy(wq).to(DEV)
+    ref_acc = og.int8_matmul_exact(xq, wq)
+    for cfg in (None, {"tile_m": 1}):
+        acc = ops.int8_gemm(a, None, w, None, out_dtype=torch.int32, config=cfg).cpu().numpy()
+        assert np.array_equal(acc, ref_acc), cfg
+    b = torch.randn(n, generator=gen(9))
+    y = ops.int8_gemm(a, torch.from_numpy(sx).to(DEV), w, torch.from_numpy(sw).to(DEV), b.to(DEV),
+                      out_dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(y, og.int8_gemm_ref(xq, sx, wq, sw, b.numpy(), acc=ref_acc))
+    y16 = ops.int8_gemm(a, torch.from_numpy(sx).to(DEV), w, torch.from_numpy(sw).to(DEV), out_dtype=torch.bfloat16)
+    ref16 = torch.from_numpy(og.int8_gemm_ref(xq, sx, wq, sw, acc=ref_acc)).bfloat16()
+    assert torch.equal(y16.cpu(), ref16)
+
+
+def test_int8_gemv_extremes_and_rejects():
+    """127 / -128 everywhere over K = 28672 (|acc| up to 4.7e8, still exact in int32); tile_m=1 rejects 3 rows."""
+    k, n = 28672, 64
+    xq = np.full((2, k), -128, dtype=np.int8)
+    xq[1, ::2] = 127
+    wq = np.full((n, k), 127, dtype=np.int8)
+    wq[::3] = -128
+    a, w = torch.from_numpy(xq).to(DEV), torch.from_numpy(wq).to(DEV)
+    acc = ops.int8_gemm(a, None, w, None, out_dtype=torch.int32, config={"tile_m": 1}).cpu().numpy()
+    assert np.array_equal(acc, og.int8_matmul_exact(xq, wq))
+    from forge_amd import _lib
+    with pytest.raises(_lib.KernelLaunchError, match="tile_m=1"):
+        ops.int8_gemm(torch.zeros(3, k, dtype=torch.int8, device=DEV), None, w, None, out_dtype=torch.int32,
+                      config={"tile_m": 1})
+
+
 @pytest.mark.parametrize("m", [0, 1, 16, 100])
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 def test_int8_linear_end_to_end(m, xdt):
