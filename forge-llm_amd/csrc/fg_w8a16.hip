@@ -9,8 +9,8 @@
 // u = q ^ 0x80 = q + 128 (0..255):
 //   fp16 x: one exact fp16 per byte, 0x6400 | u = 1024 + u (byte-permutes against the magic exponent byte), one MFMA
 //           per k-step:  sum x q = A - 1152 sum x;
-//   bf16 x: bf16 holds 128 + v exactly only for v < 128, so u splits into nibble planes h = u >> 4 and l = u & 15,
-//           each 128 + v through the magic byte, two MFMAs per k-step:  sum x q = 16 A_h + A_l - 2304 sum x.
+//   bf16 x: u itself (0..255) is exact in bf16: v_cvt_f32_ubyte{b} and a packed fp32 -> bf16 conversion, one MFMA
+//           per k-step:  sum x q = A - 128 sum x.
 // The row sums of x come from one MFMA per k-step against all-ones (in the accumulator layout); each step lies in one
 // group (group size a multiple of 128, or one group), so after a step  acc += s[n, g] * (that expression).
 //
@@ -56,6 +56,14 @@ __device__ __forceinline__ uint32_t w8a_pair_hi(uint32_t magic, uint32_t bytes) 
   return __builtin_amdgcn_perm(magic, bytes, 0x04030402u);
 }
 
+// bytes 2h, 2h + 1 of w (each < 256, exact in bf16) as one packed bf16 pair
+__device__ __forceinline__ uint32_t w8a_bf16_pair(uint32_t w, int h) {
+  typedef float f32x2_w8_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_w8_t __attribute__((ext_vector_type(2)));
+  const f32x2_w8_t f = {(float)((w >> (16 * h)) & 0xffu), (float)((w >> (16 * h + 8)) & 0xffu)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_w8_t));
+}
+
 constexpr int w8a16_max_threads(int mb, int t) { return mb * t >= 2 ? 512 : 1024; }
 
 template <int MB, int T, bool XBF16, bool SBF16>
@@ -64,7 +72,7 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
     const uint16_t* __restrict__ scales, int64_t lds, const void* __restrict__ bias, int bdt,
     uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int gsteps, int KS) {
   constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
-  constexpr float kCorr = XBF16 ? 2304.f : 1152.f;  // 17 * 128 + 128 (bf16 planes) / 1024 + 128 (fp16 bytes)
+  constexpr float kCorr = XBF16 ? 128.f : 1152.f;  // u = q + 128 (bf16) / 1024 + u = q + 1152 (fp16)
   constexpr int NV = T * MB * 4;
   extern __shared__ __align__(16) float red[];  // [waves][NV][64]
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -138,24 +146,18 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
       const float sc = SBF16 ? bf16_bits_to_f32(b.s[t]) : f16_bits_to_f32((uint16_t)b.s[t]);
       const uint32_t wd[8] = {b.w[t][0].x, b.w[t][0].y, b.w[t][0].z, b.w[t][0].w,
                               b.w[t][1].x, b.w[t][1].y, b.w[t][1].z, b.w[t][1].w};
-      f32x4_w8_t a1[MB], a2[MB];
+      f32x4_w8_t a1[MB];
 #pragma unroll
-      for (int i = 0; i < MB; ++i) a1[i] = a2[i] = f32x4_w8_t{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < MB; ++i) a1[i] = f32x4_w8_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const uint32_t u0 = wd[2 * s] ^ 0x80808080u, u1 = wd[2 * s + 1] ^ 0x80808080u;  // q + 128 per byte
         if constexpr (XBF16) {
-          const uint32_t l0 = u0 & 0x0F0F0F0Fu, l1 = u1 & 0x0F0F0F0Fu;
-          const uint32_t h0 = (u0 >> 4) & 0x0F0F0F0Fu, h1 = (u1 >> 4) & 0x0F0F0F0Fu;
-          const uint4 bl = make_uint4(w8a_pair_lo(0x43434343u, l0), w8a_pair_hi(0x43434343u, l0),
-                                      w8a_pair_lo(0x43434343u, l1), w8a_pair_hi(0x43434343u, l1));
-          const uint4 bh = make_uint4(w8a_pair_lo(0x43434343u, h0), w8a_pair_hi(0x43434343u, h0),
-                                      w8a_pair_lo(0x43434343u, h1), w8a_pair_hi(0x43434343u, h1));
+          // u (0..255) is exact in bf16: v_cvt_f32_ubyte{b} then a packed conversion, one MFMA per k-step
+          const uint4 bu = make_uint4(w8a_bf16_pair(u0, 0), w8a_bf16_pair(u0, 1), w8a_bf16_pair(u1, 0),
+                                      w8a_bf16_pair(u1, 1));
 #pragma unroll
-          for (int i = 0; i < MB; ++i) {
-            a1[i] = w8_mfma<XBF16>(b.x[i][s], bh, a1[i]);
-            a2[i] = w8_mfma<XBF16>(b.x[i][s], bl, a2[i]);
-          }
+          for (int i = 0; i < MB; ++i) a1[i] = w8_mfma<XBF16>(b.x[i][s], bu, a1[i]);
         } else {
           const uint4 bu = make_uint4(w8a_pair_lo(0x64646464u, u0), w8a_pair_hi(0x64646464u, u0),
                                       w8a_pair_lo(0x64646464u, u1), w8a_pair_hi(0x64646464u, u1));
@@ -167,8 +169,7 @@ __global__ void __launch_bounds__(w8a16_max_threads(MB, T)) w8a16_skinny_kernel(
       for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v = XBF16 ? __builtin_fmaf(16.f, a1[i][e], a2[i][e]) : a1[i][e];
-          acc[t][i][e] = __builtin_fmaf(sc, __builtin_fmaf(-kCorr, xs[i][e], v), acc[t][i][e]);
+          acc[t][i][e] = __builtin_fmaf(sc, __builtin_fmaf(-kCorr, xs[i][e], a1[i][e]), acc[t][i][e]);
         }
     }
   };
