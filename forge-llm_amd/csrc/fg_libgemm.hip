@@ -114,9 +114,25 @@ size_t w4_libgemm_workspace_bytes(int N, int K) {
 }
 
 // Whether the route applies to these operands: 16-bit x, a bias (if any) in fp32 or x's dtype, and a K hipBLASLt
-// reads with 16-byte rows.
-bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t K) {
-  return (xdt == FG_BF16 || xdt == FG_F16) && (!bias || bdt == FG_F32 || bdt == xdt) && K % 8 == 0;
+// reads with 16-byte rows.  Under graph capture only a problem whose handle and plan already exist takes it (creating
+// them may allocate or synchronise, which a capture forbids); the caller's fused kernel serves the rest.
+bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
+                   hipStream_t s) {
+  if (!((xdt == FG_BF16 || xdt == FG_F16) && (!bias || bdt == FG_F32 || bdt == xdt) && K % 8 == 0)) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) return false;
+  if (cs == hipStreamCaptureStatusNone) return true;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kLibMaxDevices) return false;
+  const int rows = chunk_rows((int)N, (int)K);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_handle[dev]) return false;
+  for (int n0 = 0; n0 < N; n0 += rows) {
+    const int nc = N - n0 < rows ? (int)(N - n0) : rows;
+    auto it = g_plans.find(PlanKey{dev, (int)M, nc, (int)K, xdt, bias ? bdt : -1, ldx, ldy});
+    if (it == g_plans.end() || !it->second.desc) return false;
+  }
+  return true;
 }
 
 hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
@@ -149,6 +165,8 @@ hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t*
       p = get_plan(PlanKey{dev, M, nc, K, xdt, bias ? bdt : -1, ldx, ldy}, h);
     }
     if (!p) return hipErrorNotSupported;
+    // the plan is shared by every call of this signature: its bias pointer is set and consumed under the lock
+    std::lock_guard<std::mutex> lk(g_mu);
     if (bias) {
       const void* bp = static_cast<const uint8_t*>(bias) + (size_t)n0 * (bdt == FG_F32 ? 4 : 2);
       if (hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)) !=

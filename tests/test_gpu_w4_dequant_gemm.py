@@ -84,3 +84,39 @@ def test_act_order_stays_on_the_fused_kernel():
     assert_close(y.cpu(), ref, "bfloat16", what="act-order m=1024")
     with pytest.raises(ForgeError):  # the sorted weight comes with a column perm
         ops.w4a16_linear(x.to(DEV), p, config={"impl": "dequant_gemm"})
+
+
+def test_graph_capture_uses_the_route_only_once_its_plan_exists():
+    """A first call captured into a HIP graph takes the fused kernel (making the hipBLASLt plan inside a capture is
+    not allowed); after an eager call of the same problem, a captured call takes the route.  Every replay, with eager
+    work between replays, equals the eager result of the same path bit for bit."""
+    m, n, k = 1024, 1536, 4096  # a problem signature no other test makes a plan for
+    q, s, z = w4_parts(n, k, 128, False, seed=41)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(m, k, torch.bfloat16, seed=42).to(DEV)
+    ref = og.w4a16_gemm_ref(to_f32(x.cpu()), oracle_packed(q, s, z, 128))
+    fused = ops.w4a16_linear(x, p, config={"impl": "prefill"})
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream), torch.cuda.graph(g1, stream=stream):
+        y1 = ops.w4a16_linear(x, p)
+    torch.cuda.current_stream().wait_stream(stream)
+    for _ in range(3):
+        g1.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y1, fused), "captured first call: not the fused kernel's bits"
+        ops.w4a16_linear(x[:7], p)  # eager work between replays
+    routed = ops.w4a16_linear(x, p)  # eager: makes the plan, takes the route
+    assert_close(routed.cpu(), ref, "bfloat16", what="route after capture")
+    assert torch.equal(routed, ops.w4a16_linear(x, p, config={"impl": "dequant_gemm"}))
+    g2 = torch.cuda.CUDAGraph()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream), torch.cuda.graph(g2, stream=stream):
+        y2 = ops.w4a16_linear(x, p)
+    torch.cuda.current_stream().wait_stream(stream)
+    for _ in range(3):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y2, routed), "captured call after the plan exists: not the route's bits"
+        ops.w4a16_linear(x[:7], p)
