@@ -16,8 +16,11 @@
 // (so the count holds), reading 0 and moving no memory.  Rows of x past M and tiles past N read out of range (0).
 //
 // Arithmetic, as w4_frag_kernel: B = magic | nibble pair ((word >> 4 p) & 0x000F000F | 0x4300 4300 for bf16, 0x6400
-// 6400 for fp16: the exact values 128 + q / 1024 + q), one v_and_or_b32 per pair (plus a shift for p > 0); x row sums
-// from MFMAs against all-ones; per step acc += s * (acc_step - (B + z) * xsum).
+// 6400 for fp16: the exact values 128 + q / 1024 + q), one v_and_or_b32 per pair (plus a shift for p > 0); per step
+// acc += s * (acc_step - (B + z) * xsum), the x row sums from MFMAs against all-ones.  The row sums of a step are the
+// same for every wavefront: on eight wavefronts, wavefront b < 4 computes those of row block b into an LDS pair buffered
+// by step parity, and every wavefront subtracts s * (B + z) * xsum one step later, after the next step's barrier has
+// made them visible (the last step's after one more barrier at the end).
 //
 // K splits (KS > 1): each split writes its fp32 partial to the caller's workspace [KS, M, N] and w4_ring_reduce_kernel
 // sums them in split order (bit-reproducible), adds the bias and rounds, eight outputs per thread.  (Letting the last
@@ -78,6 +81,8 @@ struct RingShape {
   static constexpr int W = BW * T * 1024;     // weight tiles of one step
   static constexpr int SZ = BW * 512;         // per wavefront: 256 bytes of scales, 256 of zero words
   static constexpr int STAGE = X + W + SZ;
+  static constexpr bool SHARE = MB == 4 && BW == 8;  // x row sums computed once per workgroup (w4_ring_kernel)
+  static constexpr int XS = SHARE ? 2 * MB * 16 * 4 : 0;  // the row sums of two steps (fp32), after the S stages
   static constexpr int XI = 4 * MB / BW;      // x loads (1 KiB = 4 rows each) per wavefront and step
   static constexpr int NI = XI + T + 2;       // loads per wavefront and step
 };
@@ -108,6 +113,11 @@ template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
 __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   using Sh = RingShape<MB, T, BW>;
   static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
+  // Row sums shared through LDS on eight wavefronts of 33..64 rows (wavefront b < 4 computes row block b's).  Elsewhere
+  // every wavefront computes its MB blocks' sums itself: with fewer row blocks than wavefronts wavefront 0 computes as
+  // many either way, and on four wavefronts the fewer MFMAs did not make up for the extra LDS reads of x (M = 64:
+  // qkv 17.2 -> 16.5 us, down 25.2 -> 23.7 with sharing; o_proj 14.4 -> 14.8, gate+up level on four wavefronts).
+  constexpr bool SHARE = Sh::SHARE;
   constexpr float kB = XBF16 ? 128.f : 1024.f;
   constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -184,7 +194,25 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   const uint32_t magic = XBF16 ? 0x43004300u : 0x64006400u;
   const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
 
-  auto compute = [&](const uint8_t* __restrict__ stg) __attribute__((always_inline)) {
+  // row sums by step parity: step i's are written into xsb[i % 2] and read at step i + 1
+  float* const xsb = reinterpret_cast<float*>(smem + S * Sh::STAGE);
+  if constexpr (SHARE)  // read at step 0 (times zero)
+    for (int q = (int)threadIdx.x; q < 2 * MB * 16; q += BW * kWave) xsb[q] = 0.f;
+  float szb[T];  // s * (B + z) of the previous step, per tile
+#pragma unroll
+  for (int t = 0; t < T; ++t) szb[t] = 0.f;
+
+  auto compute = [&](const uint8_t* __restrict__ stg, float* __restrict__ xsw, const float* __restrict__ xsr)
+                     __attribute__((always_inline)) {
+    if (SHARE && wave < MB) {  // first, this step's row sums of row block `wave`, for every wavefront
+      const uint8_t* xr = stg + (16 * wave + r16) * 256;
+      f32x4_rg_t xs = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        xs = rg_mfma<XBF16>(*reinterpret_cast<const uint4*>(xr + (((PORT ? 4 * j + s : 4 * s + j) ^ r16) * 16)), ones,
+                            xs);
+      if (r16 == 0) *reinterpret_cast<f32x4_rg_t*>(xsw + 16 * wave + 4 * j) = xs;
+    }
     const uint8_t* sw = stg + Sh::X;
     const uint8_t* ssz = stg + Sh::X + Sh::W + wave * 512;
     uint4 raw[T];
@@ -205,9 +233,14 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
       for (int s = 0; s < 4; ++s)
         af[s] = *reinterpret_cast<const uint4*>(stg + (16 * i + r16) * 256 +
                                                 (((PORT ? 4 * j + s : 4 * s + j) ^ r16) * 16));
-      f32x4_rg_t xs = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
+      f32x4_rg_t xp;  // SHARE: the previous step's row sums; else this step's
+      if constexpr (SHARE) {
+        xp = *reinterpret_cast<const f32x4_rg_t*>(xsr + 16 * i + 4 * j);
+      } else {
+        xp = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xs = rg_mfma<XBF16>(af[s], ones, xs);
+        for (int s = 0; s < 4; ++s) xp = rg_mfma<XBF16>(af[s], ones, xp);
+      }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         const uint32_t wq[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
@@ -218,8 +251,13 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
                               as);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          acc[t][i][e] = __builtin_fmaf(sc[t], __builtin_fmaf(-zb[t], xs[e], as[e]), acc[t][i][e]);
+          acc[t][i][e] = SHARE ? __builtin_fmaf(sc[t], as[e], __builtin_fmaf(-szb[t], xp[e], acc[t][i][e]))
+                               : __builtin_fmaf(sc[t], __builtin_fmaf(-zb[t], xp[e], as[e]), acc[t][i][e]);
       }
+    }
+    if constexpr (SHARE) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) szb[t] = sc[t] * zb[t];
     }
   };
 
@@ -230,12 +268,26 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   auto body = [&](int i, const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt) __attribute__((always_inline)) {
     issue(i + S - 1, nxt);  // the slot of step i - 1: every wavefront has read it (last barrier)
     __builtin_amdgcn_sched_barrier(0);
-    compute(cur);
+    compute(cur, xsb + (i & 1) * MB * 16, xsb + ((i + 1) & 1) * MB * 16);
   };
   for (int i = 0; i < ns; ++i) {
-    // this step's loads have landed for every wavefront, and every wavefront is done with step i - 1's slot
+    // this step's loads have landed for every wavefront, every wavefront is done with step i - 1's slot and with the
+    // row sums of step i - 2, and step i - 1's row sums are in LDS
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * Sh::NI) : "memory");
     body(i, smem + (i % S) * Sh::STAGE, smem + ((i + S - 1) % S) * Sh::STAGE);
+  }
+  // the last step's row sums
+  if constexpr (SHARE) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const float* xsr = xsb + ((ns + 1) & 1) * MB * 16;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const f32x4_rg_t xp = *reinterpret_cast<const f32x4_rg_t*>(xsr + 16 * i + 4 * j);
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][i][e] = __builtin_fmaf(-szb[t], xp[e], acc[t][i][e]);
+    }
   }
 
   // KS == 1: y (+ bias); KS > 1: this split's fp32 partial
@@ -382,7 +434,7 @@ static hipError_t launch_ring_reduce(bool xbf16, const float* part, int KS, int 
 template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
 static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
   using Sh = RingShape<MB, T, BW>;
-  const size_t shm = (size_t)S * Sh::STAGE;
+  const size_t shm = (size_t)S * Sh::STAGE + Sh::XS;
   auto kern = w4_ring_kernel<MB, T, BW, S, XBF16, SBF16, PORT>;
   if (shm > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
