@@ -894,39 +894,61 @@ __global__ void __launch_bounds__(256) w4_dequant_kernel(
   }
 }
 
-// Dense dequantisation to a 16-bit output, one thread per 32 columns of one row (16 bytes of qweight in, 64 bytes
-// out, every access a 16-byte vector): (q - z) * s = fma(q, s, -z * s), exact in fp32 (both products and their sum
-// are exact for |q - z| <= 15 and a 16-bit scale), rounded once to nearest even -- the generic kernel's value, bit
-// for bit.  Needs K % 32 == 0, groups of whole 32-column chunks (or one group), 16-bit scales, no g_idx, 16-byte
-// aligned qweight / out with ldq % 4 == 0 and ldo % 8 == 0.
+// Dense dequantisation to a 16-bit output: one wavefront per 2048 columns of one channel row, lane l converting
+// columns c0 + 512 i + 8 l .. + 7 (i = 0..3) from one dword of qweight each, so every dword load reads 256 and every
+// 16-byte store writes 1024 contiguous bytes per wavefront (a thread per 32 columns wrote 16 of every 64 bytes per
+// store instruction and ran at 2.5-3.1 TB/s).  (q - z) * s = fma(q, s, -z * s) is exact in fp32 (both products and
+// their sum are exact for |q - z| <= 15 and a 16-bit scale) and rounded once to nearest even by the packed hardware
+// conversion -- the generic kernel's value, bit for bit.  Group of column c: c / gs by a multiply-high with the host's
+// constant (gdiv = 0: one group).  Needs K % 32 == 0, groups of whole 32-column chunks (or one group), 16-bit scales,
+// no g_idx, 4-byte aligned qweight, 16-byte aligned out with ldo % 8 == 0.
 template <bool OBF16>
 __global__ void __launch_bounds__(256) w4_dequant16_kernel(const int32_t* __restrict__ qw, int64_t ldq,
                                                            const uint16_t* __restrict__ scales, int sbf16, int64_t lds,
                                                            const int32_t* __restrict__ zeros, int64_t ldz,
-                                                           uint16_t* __restrict__ out, int64_t ldo, int N, int KC,
-                                                           int gs32) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (int64_t)N * KC) return;
-  const int n = (int)(t / KC), c = (int)(t - (int64_t)n * KC);
-  const int g = gs32 > 0 ? c / gs32 : 0;
-  const uint4 w = load16_stream(qw + (int64_t)n * ldq + 4 * c);
-  const uint16_t sb = scales[(int64_t)g * lds + n];
-  const float sc = sbf16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
-  const float z = zeros ? (float)nibble((uint32_t)zeros[(int64_t)g * ldz + n / 8], n & 7) : 8.f;
-  const float cz = -z * sc;
-  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-  uint4* o = reinterpret_cast<uint4*>(out + (int64_t)n * ldo + 32 * c);
+                                                           uint16_t* __restrict__ out, int64_t ldo, int N, int K,
+                                                           int wpr, uint32_t gdiv, uint32_t gmul) {
+  typedef float f32x2_dq_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_dq_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2_dq_t __attribute__((ext_vector_type(2)));
+  const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (wv >= (int64_t)N * wpr) return;  // whole wavefronts
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = (int)(wv / wpr), c0 = (int)(wv - (int64_t)n * wpr) * 2048 + 8 * lane;
+  const int32_t* qr = qw + (int64_t)n * ldq;
+  uint16_t* orow = out + (int64_t)n * ldo;
+  uint32_t w[4];
+  float sc[4], cz[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t h[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float lo = __builtin_fmaf((float)nibble(wd[i], 2 * j), sc, cz);
-      const float hi = __builtin_fmaf((float)nibble(wd[i], 2 * j + 1), sc, cz);
-      h[j] = OBF16 ? (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16)
-                   : (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    const int c = c0 + 512 * i;
+    if (c < K) {
+      w[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(qr) + c / 8);
+      const uint32_t g = gdiv > 1 ? __umulhi((uint32_t)c, gmul) : (gdiv == 1 ? (uint32_t)c : 0u);
+      const uint16_t sb = scales[(int64_t)g * lds + n];
+      sc[i] = sbf16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
+      const float z = zeros ? (float)nibble((uint32_t)zeros[(int64_t)g * ldz + n / 8], n & 7) : 8.f;
+      cz[i] = -z * sc[i];
     }
-    o[i] = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = c0 + 512 * i;
+    if (c < K) {
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;  // nibbles 2j / 2j + 1 in byte j
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x2_dq_t v = {__builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc[i], cz[i]),
+                              __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc[i], cz[i])};
+        if constexpr (OBF16) {
+          h[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_dq_t));
+        } else {
+          h[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_dq_t));
+        }
+      }
+      *reinterpret_cast<uint4*>(orow + c) = make_uint4(h[0], h[1], h[2], h[3]);
+    }
   }
 }
 
@@ -1092,14 +1114,15 @@ hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales,
                              int N, int K, int gs, hipStream_t s) {
   const bool one_group = gs >= K;
   if (!g_idx && (odt == FG_BF16 || odt == FG_F16) && (sdt == FG_BF16 || sdt == FG_F16) && K % 32 == 0 &&
-      (gs % 32 == 0 || one_group) && ldq % 4 == 0 && reinterpret_cast<uintptr_t>(qw) % 16 == 0 && ldo % 8 == 0 &&
+      (gs % 32 == 0 || one_group) && reinterpret_cast<uintptr_t>(qw) % 4 == 0 && ldo % 8 == 0 &&
       reinterpret_cast<uintptr_t>(out) % 16 == 0) {
-    const int KC = K / 32;
-    const int64_t blocks = ((int64_t)N * KC + 255) / 256;
+    const int wpr = (K + 2047) / 2048;  // wavefronts per channel row
+    const int64_t blocks = ((int64_t)N * wpr + 3) / 4;
+    const uint32_t gdiv = one_group ? 0u : (uint32_t)gs;
+    const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;  // c / gs = umulhi(c, gmul), c < 2^31
     auto kern = odt == FG_BF16 ? w4_dequant16_kernel<true> : w4_dequant16_kernel<false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, static_cast<const uint16_t*>(scales),
-                       (int)(sdt == FG_BF16), lds, zeros, ldz, static_cast<uint16_t*>(out), ldo, N, KC,
-                       one_group ? 0 : gs / 32);
+                       (int)(sdt == FG_BF16), lds, zeros, ldz, static_cast<uint16_t*>(out), ldo, N, K, wpr, gdiv, gmul);
     return hipGetLastError();
   }
   const int64_t total = (int64_t)N * ((K + 7) / 8);
