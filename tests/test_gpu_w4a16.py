@@ -236,6 +236,21 @@ def test_dequant_is_bit_exact(scale_dtype, out, sym, gs):
         assert torch.equal(d, torch.from_numpy(ref).to(out))  # one rounding of the exact fp32 value
 
 
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k,sym,gs", [(1024, False, 128), (4160, True, 32), (6144, False, -1), (2048, True, 128)])
+def test_dequant_16bit_fast_path_is_bit_exact(scale_dtype, out, k, sym, gs):
+    """The dense 16-bit dequantisation (K % 32 == 0, whole 32-column groups or one group, 16-bit scales): one
+    wavefront per 2048 columns of a row, so K = 1024 leaves most lanes idle, 4160 ends in a 64-column wavefront and
+    6144 spans three; every value is the exact fp32 (q - z) * s rounded once."""
+    n = 136
+    q, s, z = w4_parts(n, k, gs, sym, seed=k + 3, scale_dtype=scale_dtype)
+    p = L.pack_w4(q, s, z, gs).to(DEV)
+    d = p.dequantize(out).cpu()
+    ref = ow.dequantize_parts(q.numpy(), s.float().numpy(), None if z is None else z.numpy(), gs)
+    assert torch.equal(d, torch.from_numpy(ref).to(out))
+
+
 @pytest.mark.parametrize("kn", [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)])
 @pytest.mark.parametrize("m", [1, 16])
 def test_llama3_8b_decode_shapes(kn, m):
