@@ -87,10 +87,12 @@ def test_cdna4_module_and_c_abi_rejections():
 
 
 # The LDS-ring kernel: 33..64 rows, or 9..64 rows over K >= 8192 (N % 16 == 0); K-split plans with a reduce launch
-# (small N, long K) and without (wide N), one group / several groups per step, symmetric, fp16 x, bf16 scales, bias.
+# (small N, long K) and without (wide N), one group / several groups per step, symmetric, fp16 x, bf16 scales, bias;
+# splits of 1..32 steps, so the four-wavefront loop (unrolled by its 3-stage ring) ends with 0, 1 and 2 leftover steps.
 @pytest.mark.parametrize("m,n,k,gs", [(33, 2048, 4096, 128), (40, 4096, 4096, 256), (64, 1024, 2048, -1),
                                       (64, 16384, 4096, 128), (48, 512, 8192, 128), (12, 4096, 8192, 256),
-                                      (16, 4096, 14336, 128), (24, 1024, 16384, -1), (64, 4096, 14336, 128)])
+                                      (16, 4096, 14336, 128), (24, 1024, 16384, -1), (64, 4096, 14336, 128),
+                                      (40, 2048, 6144, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_cdna4_ring_kernel(m, n, k, gs, xdt):
     sdt = torch.bfloat16 if m % 2 else torch.float16
