@@ -40,6 +40,13 @@ hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int
 hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq,
                                 const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
                                 int64_t ldy, int M, int N, int K, int gs, hipStream_t s);
+bool w8a16_ring_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt,
+                   int64_t lds, int64_t M, int64_t N, int64_t K, int gs, int64_t G);
+size_t w8a16_ring_workspace_bytes(int M, int N, int K);
+hipError_t launch_w8a16_ring(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                             const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy,
+                             int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
+                             hipStream_t s);
 bool w8a16_gemv_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt,
                    int64_t lds, int64_t M, int64_t N, int64_t K, int gs, int64_t G);
 hipError_t launch_w8a16_gemv(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
@@ -603,6 +610,15 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
                     "fg_w4_dequant launch");
 }
 
+// Whether the automatic W8A16 policy takes the LDS-ring kernel (when its conditions hold): 17..64 rows, and 3..16 rows
+// over wide or long weights.  Graph replays over a 1.2 GB weight ring, us, ring / skinny: M = 64 qkv 18.4 / 37.9,
+// o_proj 14.4 / 21.1, gate+up 44.4 / 143.5, down 27.2 / 61.2; M = 32 13.9 / 16.1, 10.9 / 13.0, 31.5 / 51.9,
+// 21.5 / 36.0; M = 16 11.9 / 11.7, 9.5 / 9.1, 26.9 / 30.7, 17.9 / 23.7; M = 3 11.3 / 9.8, 9.3 / 7.5, 28.0 / 29.1,
+// 17.1 / 18.3.
+static bool w8a16_ring_rows(int64_t M, int64_t N, int64_t K) {
+  return M > 16 ? M <= 64 : (M > 2 && (N >= 16384 || K >= 8192));
+}
+
 size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, const fg_w4_config* cfg) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
   const int gs = group_size > 0 ? group_size : (int)K;
@@ -611,7 +627,9 @@ size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   // the prefill kernel's split-K partials, whenever it may run (its alignment conditions are checked at launch)
   const bool prefill_shape = (K % 64 == 0) && (gs % 32 == 0 || G == 1);
   if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return 0;
-  return fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0);
+  const size_t ring = impl == FG_W4_AUTO && w8a16_ring_rows(M, N, K) ? fg::w8a16_ring_workspace_bytes((int)M, (int)N, (int)K)
+                                                               : 0;
+  return std::max(ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0));
 }
 
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
@@ -639,14 +657,17 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
   const bool gemv = fg::w8a16_gemv_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);
   const bool big = fg::w8_big_ok(x, ldx, qweight, ldq, K, gs, G);
+  const bool ring = fg::w8a16_ring_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   int kern = impl == FG_W4_GENERIC ? 0
              : impl == FG_W4_MFMA  ? 1
              : impl == FG_W4_PREFILL ? 2
              : impl == FG_W4_GEMV  ? 3
                                    : -1;
   // 1..2 rows: the decode GEMV (graph replays, M = 1, us, GEMV / skinny: qkv 6.2 / 9.6, o_proj 5.1 / 8.0, gate+up
-  // 20.7 / 28.7, down 12.6 / 17.3; M = 4 gate+up 34.4 / 27.7, so 3..64 rows stay on the skinny kernel)
-  if (kern < 0) kern = (gemv && M <= 2) ? 3 : ((skinny && M <= 64) ? 1 : (big ? 2 : 0));
+  // 20.7 / 28.7, down 12.6 / 17.3; M = 4 gate+up 34.4 / 27.7); then the LDS ring (w8a16_ring_rows), else the skinny
+  // kernel up to 64 rows
+  if (kern < 0)
+    kern = (gemv && M <= 2) ? 3 : ((ring && w8a16_ring_rows(M, N, K)) ? 4 : ((skinny && M <= 64) ? 1 : (big ? 2 : 0)));
   if (kern == 3 && !gemv)
     return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: decode GEMV needs M<=4, K%%16==0, group%%16==0 (or one group), "
                                  "16-bit scales with lds%%8==0, ldq%%16==0, ldx%%8==0, 16-byte aligned x/qweight/"
@@ -658,7 +679,14 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: prefill kernel needs K%%64==0, group%%32==0 (or one group), "
                                  "ldq%%16==0, ldx%%8==0 and 16-byte aligned x/qweight");
   hipError_t e;
-  if (kern == 3) {
+  if (kern == 4) {
+    const size_t need = fg::w8a16_ring_workspace_bytes((int)M, (int)N, (int)K);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      return fail(FG_EINVAL, "fg_w8a16_gemm: workspace of %zu bytes needed, %zu given", need,
+                  workspace ? workspace_bytes : (size_t)0);
+    e = fg::launch_w8a16_ring(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy, (int)M,
+                              (int)N, (int)K, gs, G == 1, (int)G, workspace, workspace_bytes, s);
+  } else if (kern == 3) {
     e = fg::launch_w8a16_gemv(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy, (int)M,
                               (int)N, (int)K, gs, G == 1, G, s);
   } else if (kern == 1) {

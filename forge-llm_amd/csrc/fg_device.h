@@ -240,6 +240,23 @@ __device__ __forceinline__ uint4 load16_stream(const void* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// int8 weights as exact 16-bit values (u = q ^ 0x80 = q + 128, 0..255, used by the W8A16 kernels).
+// four bytes b0..b3 (each < 256) as two 16-bit pairs (M + b0, M + b1), (M + b2, M + b3) above the magic byte M
+__device__ __forceinline__ uint32_t w8a_pair_lo(uint32_t magic, uint32_t bytes) {
+  return __builtin_amdgcn_perm(magic, bytes, 0x04010400u);
+}
+__device__ __forceinline__ uint32_t w8a_pair_hi(uint32_t magic, uint32_t bytes) {
+  return __builtin_amdgcn_perm(magic, bytes, 0x04030402u);
+}
+
+// bytes 2h, 2h + 1 of w (each < 256, exact in bf16) as one packed bf16 pair
+__device__ __forceinline__ uint32_t w8a_bf16_pair(uint32_t w, int h) {
+  typedef float f32x2_w8_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_w8_t __attribute__((ext_vector_type(2)));
+  const f32x2_w8_t f = {(float)((w >> (16 * h)) & 0xffu), (float)((w >> (16 * h + 8)) & 0xffu)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_w8_t));
+}
+
 // nibble j (bits 4j..4j+3) of a packed word
 __device__ __forceinline__ uint32_t nibble(uint32_t w, int j) { return (w >> (4 * j)) & 0xFu; }
 

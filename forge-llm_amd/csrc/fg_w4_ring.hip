@@ -74,24 +74,30 @@ __device__ __forceinline__ uint4 rg_unpack_portable(uint32_t w, uint32_t mask, u
                     rg_and_or(__builtin_amdgcn_perm(h, w, 0x0C070C03u), mask, magic));
 }
 
-template <int MB, int T, int BW>
+template <int MB, int T, int BW, bool W8 = false>
 struct RingShape {
   static_assert((4 * MB) % BW == 0, "the x rows of a step split evenly over the wavefronts");
   static constexpr int X = MB * 16 * 256;     // x rows of one step
-  static constexpr int W = BW * T * 1024;     // weight tiles of one step
-  static constexpr int SZ = BW * 512;         // per wavefront: 256 bytes of scales, 256 of zero words
+  static constexpr int TB = W8 ? 2048 : 1024;  // one 16-channel tile's weights per step
+  static constexpr int W = BW * T * TB;       // weight tiles of one step
+  static constexpr int SB = W8 ? 256 : 512;   // per wavefront: 256 bytes of scales (+ 256 of zero words for W4)
+  static constexpr int SZ = BW * SB;
   static constexpr int STAGE = X + W + SZ;
   static constexpr bool SHARE = MB == 4 && BW == 8;  // x row sums computed once per workgroup (w4_ring_kernel)
   static constexpr int XS = SHARE ? 2 * MB * 16 * 4 : 0;  // the row sums of two steps (fp32), after the S stages
   static constexpr int XI = 4 * MB / BW;      // x loads (1 KiB = 4 rows each) per wavefront and step
-  static constexpr int NI = XI + T + 2;       // loads per wavefront and step
+  static constexpr int NI = XI + (W8 ? 2 * T + 1 : T + 2);  // loads per wavefront and step
 };
+
+// Swizzle of a W8 tile's 128-byte rows in LDS: 16-byte unit u of row r at position u ^ key (the units 2 j, 2 j + 1
+// that lane group j reads of 16 rows fall on distinct bank groups; the same key as the FP8 MFMA operand's rows).
+__device__ __forceinline__ int w8_ring_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 struct RingArgs {
   const uint16_t* x;
   int64_t ldx;
   const int32_t* qw;
-  int64_t ldq;  // int32 words per 16-channel tile row
+  int64_t ldq;  // W4: int32 words per row (portable) or per 16-channel tile row (CDNA4); W8: bytes per row
   const uint16_t* scales;
   int64_t lds;
   const int32_t* zeros;
@@ -104,14 +110,20 @@ struct RingArgs {
   uint32_t qbytes, xbytes, sbytes, zbytes;
 };
 
-// PORT: weights in portable_row ([N, ldq] int32 words, row n = channel n): a tile's step is 16 rows x 64 bytes,
+// FMT 1: W4 weights in portable_row ([N, ldq] int32 words, row n = channel n): a tile's step is 16 rows x 64 bytes,
 // loaded into LDS row by row with the 16-byte quarter q of row r at position q ^ ((r / 4) % 4) (the 16 rows of one
 // B read fall on distinct bank groups), and lane group j takes quarter j: MFMA k-step s of lane group j is word 4 j + s
 // (columns 32 j + 8 s ..), so x's unit 4 j + s goes with it (the sum over K does not care which 32 columns go to
-// which k-step).  Otherwise the CDNA4 layout: lane l's 16 bytes at l * 16, k-step s = word s (columns 32 s + 8 j ..).
-template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
-__global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
-  using Sh = RingShape<MB, T, BW>;
+// which k-step).  FMT 0: the CDNA4 layout: lane l's 16 bytes at l * 16, k-step s = word s (columns 32 s + 8 j ..).
+// FMT 2: W8A16 weights (int8 [N, ldq] bytes, symmetric, scales [G, N]): a tile's step is 16 rows x 128 bytes (two
+// loads), unit u of row r at position u ^ w8_ring_key(r); lane group j reads units 2 j, 2 j + 1 of its row, the
+// 32 bytes of columns 32 j .. 32 j + 31, k-step s takes bytes 8 s .. 8 s + 7 (x's unit 4 j + s, as for FMT 1).  A
+// byte q becomes u = q ^ 0x80 = q + 128, exact as a bf16 (0..255) or, for fp16 x, as 1024 + u above the magic
+// exponent byte, so  sum x q = sum x B - (128 or 1152) sum x  in place of W4's  - (B + z) sum x.
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, int FMT>
+__device__ __forceinline__ void ring_body(const RingArgs& a) {
+  constexpr bool PORT = FMT != 0, W8 = FMT == 2;
+  using Sh = RingShape<MB, T, BW, W8>;
   static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
   // Row sums shared through LDS on eight wavefronts of 33..64 rows (wavefront b < 4 computes row block b's).  Elsewhere
   // every wavefront computes its MB blocks' sums itself: with fewer row blocks than wavefronts wavefront 0 computes as
@@ -119,6 +131,7 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
   // qkv 17.2 -> 16.5 us, down 25.2 -> 23.7 with sharing; o_proj 14.4 -> 14.8, gate+up level on four wavefronts).
   constexpr bool SHARE = Sh::SHARE;
   constexpr float kB = XBF16 ? 128.f : 1024.f;
+  constexpr float kCorr8 = XBF16 ? 128.f : 1152.f;  // W8: B = q + 128 (bf16) / 1024 + q + 128 (fp16)
   constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
   extern __shared__ __align__(16) uint8_t smem[];
 
@@ -144,16 +157,25 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
     const int u = (lane & 15) ^ (row & 15);
     xv[q] = row < a.M ? (uint32_t)row * (uint32_t)a.ldx * 2u + 16u * (uint32_t)u : a.xbytes;
   }
-  uint32_t wv[T];
+  constexpr int WH = W8 ? 2 : 1;  // weight loads per tile and step
+  uint32_t wv[T][WH];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    if constexpr (PORT) {  // LDS position lane = row lane / 4, slot lane % 4, holding quarter slot ^ (row / 4 % 4)
+    if constexpr (W8) {  // load h: LDS position lane = row 8 h + lane / 8, slot lane % 8, holding unit slot ^ key(row)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = 8 * h + (lane >> 3), unit = (lane & 7) ^ w8_ring_key(row);
+        wv[t][h] = tile0 + t < NT
+                       ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq + 16u * (uint32_t)unit
+                       : a.qbytes;
+      }
+    } else if constexpr (PORT) {  // LDS position lane = row lane / 4, slot lane % 4, holding quarter slot ^ (row / 4 % 4)
       const int row = lane >> 2, quarter = (lane & 3) ^ ((lane >> 4) & 3);
-      wv[t] = tile0 + t < NT
-                  ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)quarter
-                  : a.qbytes;
+      wv[t][0] = tile0 + t < NT
+                     ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)quarter
+                     : a.qbytes;
     } else {
-      wv[t] = tile0 + t < NT ? (uint32_t)(tile0 + t) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)lane : a.qbytes;
+      wv[t][0] = tile0 + t < NT ? (uint32_t)(tile0 + t) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)lane : a.qbytes;
     }
   }
   // scales: lane i < 8 T loads the channel pair 2i, 2i + 1 of the wavefront's tiles; zero words: lane i < 2 T loads
@@ -176,13 +198,16 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
                                                st * 256, 0, 0);
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(q_, (lds_void_t*)(stg + Sh::X + (wave * T + t) * 1024), 16,
-                                               (int)wv[t], st * (PORT ? 64 : 1024), 0, 2);
+#pragma unroll
+      for (int h = 0; h < WH; ++h)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(q_, (lds_void_t*)(stg + Sh::X + (wave * T + t) * Sh::TB + h * 1024),
+                                                 16, (int)wv[t][h], st * (W8 ? 128 : (PORT ? 64 : 1024)), 0, 2);
     // the group row goes into the per-lane offset (past-the-end lanes must stay past the end)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * 512), 4,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * Sh::SB), 4,
                                              sl ? (int)(g * lds2 + sv) : (int)a.sbytes, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(z_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * 512 + 256), 4,
-                                             zl ? (int)(g * ldz4 + zv) : (int)a.zbytes, 0, 0, 0);
+    if constexpr (!W8)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(z_, (lds_void_t*)(stg + Sh::X + Sh::W + wave * Sh::SB + 256), 4,
+                                               zl ? (int)(g * ldz4 + zv) : (int)a.zbytes, 0, 0, 0);
   };
 
   f32x4_rg_t acc[T][MB];
@@ -214,17 +239,28 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
       if (r16 == 0) *reinterpret_cast<f32x4_rg_t*>(xsw + 16 * wave + 4 * j) = xs;
     }
     const uint8_t* sw = stg + Sh::X;
-    const uint8_t* ssz = stg + Sh::X + Sh::W + wave * 512;
-    uint4 raw[T];
+    const uint8_t* ssz = stg + Sh::X + Sh::W + wave * Sh::SB;
+    uint4 raw[T][WH];
     float sc[T], zb[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const int wpos = PORT ? r16 * 64 + ((j ^ ((r16 >> 2) & 3)) * 16) : lane * 16;
-      raw[t] = *reinterpret_cast<const uint4*>(sw + (wave * T + t) * 1024 + wpos);
+      if constexpr (W8) {
+        const uint8_t* tr = sw + (wave * T + t) * Sh::TB + r16 * 128;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          raw[t][h] = *reinterpret_cast<const uint4*>(tr + (((2 * j + h) ^ w8_ring_key(r16)) * 16));
+      } else {
+        const int wpos = PORT ? r16 * 64 + ((j ^ ((r16 >> 2) & 3)) * 16) : lane * 16;
+        raw[t][0] = *reinterpret_cast<const uint4*>(sw + (wave * T + t) * 1024 + wpos);
+      }
       const uint16_t sb = reinterpret_cast<const uint16_t*>(ssz)[t * 16 + r16];
       sc[t] = SBF16 ? bf16_bits_to_f32(sb) : f16_bits_to_f32(sb);
-      const uint32_t zw = reinterpret_cast<const uint32_t*>(ssz + 256)[t * 2 + (r16 >> 3)];
-      zb[t] = kB + (a.hasz ? (float)nibble(zw, r16 & 7) : 8.f);
+      if constexpr (W8) {
+        zb[t] = kCorr8;
+      } else {
+        const uint32_t zw = reinterpret_cast<const uint32_t*>(ssz + 256)[t * 2 + (r16 >> 3)];
+        zb[t] = kB + (a.hasz ? (float)nibble(zw, r16 & 7) : 8.f);
+      }
     }
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
@@ -243,12 +279,24 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const uint32_t wq[4] = {raw[t].x, raw[t].y, raw[t].z, raw[t].w};
         f32x4_rg_t as = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          as = rg_mfma<XBF16>(af[s], PORT ? rg_unpack_portable(wq[s], mask, magic) : rg_unpack(wq[s], mask, magic),
-                              as);
+        for (int s = 0; s < 4; ++s) {
+          uint4 bop;
+          if constexpr (W8) {  // bytes 8 s .. 8 s + 7 of the lane's 32
+            const uint4 rw = raw[t][s >> 1];
+            const uint32_t u0 = ((s & 1) ? rw.z : rw.x) ^ 0x80808080u, u1 = ((s & 1) ? rw.w : rw.y) ^ 0x80808080u;
+            bop = XBF16 ? make_uint4(w8a_bf16_pair(u0, 0), w8a_bf16_pair(u0, 1), w8a_bf16_pair(u1, 0),
+                                     w8a_bf16_pair(u1, 1))
+                        : make_uint4(w8a_pair_lo(0x64646464u, u0), w8a_pair_hi(0x64646464u, u0),
+                                     w8a_pair_lo(0x64646464u, u1), w8a_pair_hi(0x64646464u, u1));
+          } else {
+            const uint4 rw = raw[t][0];
+            const uint32_t wq = s == 0 ? rw.x : (s == 1 ? rw.y : (s == 2 ? rw.z : rw.w));
+            bop = PORT ? rg_unpack_portable(wq, mask, magic) : rg_unpack(wq, mask, magic);
+          }
+          as = rg_mfma<XBF16>(af[s], bop, as);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[t][i][e] = SHARE ? __builtin_fmaf(sc[t], as[e], __builtin_fmaf(-szb[t], xp[e], acc[t][i][e]))
@@ -330,6 +378,17 @@ __global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
           }
         }
       }
+}
+
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16, bool PORT>
+__global__ void __launch_bounds__(BW * kWave) w4_ring_kernel(RingArgs a) {
+  ring_body<MB, T, BW, S, XBF16, SBF16, PORT ? 1 : 0>(a);
+}
+
+// W8A16 (int8 weight-only, portable [N, K] bytes) for 1..64 rows of x: the same LDS ring (FMT 2 above).
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+__global__ void __launch_bounds__(BW * kWave) w8a16_ring_kernel(RingArgs a) {
+  ring_body<MB, T, BW, S, XBF16, SBF16, 2>(a);
 }
 
 // y[m, n .. n + 7] = sum over the KS partials in split order (+ bias), one thread per 8 outputs (N % 16 == 0).  The
@@ -517,6 +576,89 @@ hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16,
     return hipErrorInvalidValue;
   const bool sbf = sdt == FG_BF16;
   const hipError_t e = portable ? launch_ring_p<true>(xbf16, sbf, p, a, s) : launch_ring_p<false>(xbf16, sbf, p, a, s);
+  if (e != hipSuccess || p.KS == 1) return e;
+  return launch_ring_reduce(xbf16, a.part, p.KS, M, N, bias, bdt, y, ldy, s);
+}
+
+// ------------------------------------------------------------------------------------------------ W8A16 ring
+// int8 [N, ldq] weights (ldq bytes per row, a multiple of 16), scales [G, lds] 16-bit, no zero-points.
+bool w8a16_ring_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt,
+                   int64_t lds, int64_t M, int64_t N, int64_t K, int gs, int64_t G) {
+  const int64_t k2g = 1LL << 31;  // offsets past a span plus a step offset stay below 2^32
+  return M > 0 && M <= 64 && sdt != FG_F32 && N % 16 == 0 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) &&
+         (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 && ldq >= K &&
+         (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
+         (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && N * ldq < k2g && M * ldx * 2 < k2g && G * lds * 2 < k2g;
+}
+
+size_t w8a16_ring_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || M > 64 || N % 16 != 0 || K % 128 != 0) return 0;
+  const RingPlan p = w4_ring_plan(M, N, K);
+  return p.KS == 1 ? 0 : (size_t)p.KS * M * N * sizeof(float);
+}
+
+template <int MB, int T, int BW, int S, bool XBF16, bool SBF16>
+static hipError_t launch_w8ring_t(const RingArgs& a, hipStream_t s) {
+  using Sh = RingShape<MB, T, BW, true>;
+  const size_t shm = (size_t)S * Sh::STAGE + Sh::XS;
+  auto kern = w8a16_ring_kernel<MB, T, BW, S, XBF16, SBF16>;
+  if (shm > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(a.ngrp * a.KS), dim3(BW * kWave), shm, s, a);
+  return hipGetLastError();
+}
+
+template <bool XBF16, bool SBF16>
+static hipError_t launch_w8ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
+  if (p.mb == 1) return launch_w8ring_t<1, 1, 4, 4, XBF16, SBF16>(a, s);
+  if (p.mb == 2) return launch_w8ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
+  if (p.T == 2) return launch_w8ring_t<4, 2, 4, 3, XBF16, SBF16>(a, s);
+  return p.BW == 8 ? launch_w8ring_t<4, 1, 8, 3, XBF16, SBF16>(a, s) : launch_w8ring_t<4, 1, 4, 3, XBF16, SBF16>(a, s);
+}
+
+hipError_t launch_w8a16_ring(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
+                             const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy,
+                             int M, int N, int K, int gs, bool single_group, int G, void* ws, size_t ws_bytes,
+                             hipStream_t s) {
+  const RingPlan p = w4_ring_plan(M, N, K);
+  RingArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.qw = reinterpret_cast<const int32_t*>(qw);
+  a.ldq = ldq;
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.lds = lds;
+  a.hasz = 0;
+  a.zeros = a.qw;  // never read (no zero-point loads in the W8 form)
+  a.ldz = 0;
+  a.bias = bias;
+  a.bdt = bdt;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.gsteps = single_group ? 0 : gs / 128;
+  a.KS = p.KS;
+  a.ngrp = p.ngrp;
+  a.qbytes = (uint32_t)((int64_t)N * ldq);
+  a.xbytes = (uint32_t)((int64_t)M * ldx * 2);
+  a.sbytes = (uint32_t)((int64_t)G * lds * 2);
+  a.zbytes = 0;
+  a.part = static_cast<float*>(ws);
+  if (p.KS > 1 && (ws == nullptr || ws_bytes < (size_t)p.KS * M * N * sizeof(float) ||
+                   reinterpret_cast<uintptr_t>(ws) % 16 != 0))
+    return hipErrorInvalidValue;
+  const bool sbf = sdt == FG_BF16;
+  hipError_t e;
+  if (xbf16) {
+    e = sbf ? launch_w8ring_x<true, true>(p, a, s) : launch_w8ring_x<true, false>(p, a, s);
+  } else {
+    e = sbf ? launch_w8ring_x<false, true>(p, a, s) : launch_w8ring_x<false, false>(p, a, s);
+  }
   if (e != hipSuccess || p.KS == 1) return e;
   return launch_ring_reduce(xbf16, a.part, p.KS, M, N, bias, bdt, y, ldy, s);
 }

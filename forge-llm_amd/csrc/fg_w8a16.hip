@@ -48,22 +48,6 @@ __device__ __forceinline__ uint4 w8a_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// four bytes b0..b3 (each < 256) as two 16-bit pairs (M + b0, M + b1), (M + b2, M + b3) above the magic byte M
-__device__ __forceinline__ uint32_t w8a_pair_lo(uint32_t magic, uint32_t bytes) {
-  return __builtin_amdgcn_perm(magic, bytes, 0x04010400u);
-}
-__device__ __forceinline__ uint32_t w8a_pair_hi(uint32_t magic, uint32_t bytes) {
-  return __builtin_amdgcn_perm(magic, bytes, 0x04030402u);
-}
-
-// bytes 2h, 2h + 1 of w (each < 256, exact in bf16) as one packed bf16 pair
-__device__ __forceinline__ uint32_t w8a_bf16_pair(uint32_t w, int h) {
-  typedef float f32x2_w8_t __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2_w8_t __attribute__((ext_vector_type(2)));
-  const f32x2_w8_t f = {(float)((w >> (16 * h)) & 0xffu), (float)((w >> (16 * h + 8)) & 0xffu)};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_w8_t));
-}
-
 constexpr int w8a16_max_threads(int mb, int t) { return mb * t >= 2 ? 512 : 1024; }
 
 template <int MB, int T, bool XBF16, bool SBF16>

@@ -1,5 +1,5 @@
-"""GPU parity of W8A16 (fg_w8a16_gemm through the C ABI: decode GEMV, skinny MFMA, dequantise-to-LDS prefill and generic
-kernels)
+"""GPU parity of W8A16 (fg_w8a16_gemm through the C ABI: decode GEMV, LDS-ring and skinny MFMA, dequantise-to-LDS
+prefill and generic kernels)
 against the CPU oracle (forge/kernels/ref/gemm_w4a16.py:45-52 restated in oracle/gemm.py).  Bar: max|y - ref| /
 max|ref| <= 1e-2 of the fp32 oracle and the reference's compare() rule for bf16 / fp16 outputs."""
 from __future__ import annotations
@@ -45,6 +45,30 @@ def test_skinny_matches_oracle(m, n, k, gs, xdt):
     sdt = torch.bfloat16 if m % 2 else torch.float16
     y, ref = _case(m, n, k, gs, xdt, sdt=sdt, seed=m + n, config={"impl": "mfma"})
     assert_close(y.cpu(), ref, ODT[xdt], what=f"w8a16 skinny m={m} n={n} k={k} gs={gs}")
+
+
+# The LDS-ring kernel through the automatic policy (17..64 rows, and 3..16 over N >= 16384 or K >= 8192), one case per
+# launch shape: one row block (K split 16 ways + reduce / whole K), two, four on four wavefronts, four with two tiles per
+# wavefront, four on eight wavefronts (row sums shared through LDS; wide N / long K), one group per row, bias or not.
+@pytest.mark.parametrize("m,n,k,gs", [(5, 16384, 1024, 128), (12, 1024, 8192, 256), (17, 2048, 2048, -1),
+                                      (40, 4096, 4096, 128), (64, 16384, 1024, 128), (33, 6144, 2048, 128),
+                                      (64, 1024, 8192, 128)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_ring_matches_oracle(m, n, k, gs, xdt):
+    sdt = torch.bfloat16 if m % 2 else torch.float16
+    y, ref = _case(m, n, k, gs, xdt, sdt=sdt, bias=(m % 3 != 0), seed=m + n + k)
+    assert_close(y.cpu(), ref, ODT[xdt], what=f"w8a16 ring m={m} n={n} k={k} gs={gs}")
+
+
+def test_ring_reproducible_and_level_with_skinny():
+    q, s = _w8(6144, 2048, 128, seed=81)
+    p = L.pack_w8(q, s, 128).to(DEV)
+    x = x_act(48, 2048, seed=82).to(DEV)
+    runs = [ops.w8a16_linear(x, p) for _ in range(3)]
+    assert all(torch.equal(runs[0], r) for r in runs[1:])
+    ref = og.w8a16_gemm_ref(to_f32(x.cpu()), og.pack_w8(q.numpy(), s.float().numpy(), 128))
+    assert_close(runs[0].cpu(), ref, "bfloat16", what="w8a16 ring m=48")
+    assert_close(ops.w8a16_linear(x, p, config={"impl": "mfma"}).cpu(), ref, "bfloat16", what="w8a16 skinny m=48")
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
@@ -132,7 +156,7 @@ def test_split_k_reproducible_rejects_and_modules():
 
 
 @pytest.mark.parametrize("kn", [(4096, 6144), (4096, 28672), (14336, 4096)])
-@pytest.mark.parametrize("m", [1, 16])
+@pytest.mark.parametrize("m", [1, 16, 64])
 def test_llama3_8b_shapes(kn, m):
     k, n = kn
     y, ref = _case(m, n, k, -1, torch.bfloat16, bias=False, seed=k + n)

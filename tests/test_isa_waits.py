@@ -7,7 +7,9 @@ that later loads may stay in flight.  That is only correct while the instruction
 * mm_ring_kernel (W8A8 small M, S-stage ring): each loop iteration issues exactly the NI direct-to-LDS loads of one
   slice and no other vector-memory load, and waits with vmcnt((S - 2) * NI) ("slice kt + 1 has landed");
 * w4_ring_kernel (W4 on the CDNA4 layout, 33..64 rows or long K): the same rule with NI = 4 MB / BW + T + 2 buffer
-  loads into LDS per step.
+  loads into LDS per step;
+* w8a16_ring_kernel (W8A16, 3..64 rows): the same rule with NI = 4 MB / BW + 2 T + 1 (two loads per weight tile, no
+  zero-points).
 
 A compiler that reorders, splits or adds a load there breaks the check here, on the CPU, instead of silently racing on
 the GPU.  No GPU is used."""
@@ -241,3 +243,13 @@ def test_w4_ring_kernel_loop_issues_one_step_and_waits_for_the_next(kernels):
         mb, t, bw, s = (int(v) for v in re.findall(r"Li(\d+)E", name)[:4])
         found += _check_ring_loops(name, code, 4 * mb // bw + t + 2, s)
     assert found >= 16, f"expected the W4 ring instances' loops, checked {found}"
+
+
+def test_w8a16_ring_kernel_loop_issues_one_step_and_waits_for_the_next(kernels):
+    found = 0
+    for name, code in kernels.items():
+        if "w8a16_ring_kernel" not in name:
+            continue
+        mb, t, bw, s = (int(v) for v in re.findall(r"Li(\d+)E", name)[:4])
+        found += _check_ring_loops(name, code, 4 * mb // bw + 2 * t + 1, s)
+    assert found >= 16, f"expected the W8A16 ring instances' loops, checked {found}"
