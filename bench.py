@@ -194,7 +194,7 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
 
 
 def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -> dict:
-    """W8A16 (int8 weight-only, per-channel fp16 scales) decode on the four Llama-3-8B shapes at M in {1, 16}: HBM
+    """W8A16 (int8 weight-only, per-channel fp16 scales) decode on the four Llama-3-8B shapes at M in {1, 16, 64}: HBM
     GB/s of algorithmic bytes (N*K weights + 2*N scales + 2*M*K + 2*M*N), HIP-graph replays over a ring of distinct
     weights (at least 1.2 GB per shape)."""
     out = {}
@@ -204,7 +204,7 @@ def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -
                                  (torch.rand(1, n, device=dev, generator=gen) * 0.018 + 0.002).half(),
                                  layouts.PORTABLE_W8, n, k, -1) for _ in range(nring)]
         row = {}
-        for m in (1, 16):
+        for m in (1, 16, 64):
             x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
 
             def run(x=x, ring=ring):

@@ -1,6 +1,9 @@
 // W8A16 (int8 weight-only): y[M,N] = x[M,K] @ dequant(W)[N,K]^T (+bias), W[n,k] = q[n,k] * s[g(k), n], q signed int8
 // (symmetric, no zero-point), x bf16 / fp16.  The portable_row W8 layout: qweight int8 [N, K] row-major, scales [G, N].
 //
+// The policy (fg_w8a16_gemm) runs 17..64 rows, and 3..16 rows over N >= 16384 or K >= 8192, on the W4 LDS-ring kernel's
+// int8 form (w8a16_ring_kernel, fg_w4_ring.hip); the skinny kernel below serves the other 3..64-row calls.
+//
 // Skinny kernel (M <= 64): the W4 skinny kernel's split-K structure (a wavefront owns T tiles of 16 channels and one K
 // slice in 128-column steps; KS slices per workgroup summed in slice order through LDS; operands straight from global
 // memory into registers by raw buffer loads, two steps ahead).  Lane l (row l % 16, lane group j = l / 16) loads the
