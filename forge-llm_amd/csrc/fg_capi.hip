@@ -254,11 +254,11 @@ constexpr int64_t kPrefillMinM = 33;
 // 1711 / 1302; M = 512 fused ahead (down 97 / 133).
 int64_t dequant_gemm_min_m(int64_t N, int64_t K) { return N * K > (64LL << 20) ? 1536 : 1024; }
 
-// Whether the automatic policy sends a 9..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
-// 13..16 over N >= 16384 and 9..12 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
+// Whether the automatic policy sends a 4..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
+// 4..16 over N >= 16384 and 9..16 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
 // / previous choice: M = 64 qkv 17.8 / 22.4, o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 32
-// gate+up 31.4 / 44.4; M = 16 down 14.4 / 20.3), when its shape conditions can hold (N % 16 == 0, K % 128 == 0,
-// group % 128 == 0 or one group); the operands decide the rest at launch.
+// gate+up 31.4 / 44.4; M = 16 down 14.4 / 20.3; M = 4 gate+up 22.0 / 23.8), when its shape conditions can hold
+// (N % 16 == 0, K % 128 == 0, group % 128 == 0 or one group); the operands decide the rest at launch.
 bool ring_policy(const fg_w4_config* cfg, int64_t M, int64_t N, int64_t K) {
   return (!cfg || (cfg->impl == FG_W4_AUTO && !cfg->tile_m && !cfg->split_k)) && M <= 64 && N % 16 == 0 &&
          K % 128 == 0 && fg::w4_ring_preferred(true, (int)M, (int)N, (int)K);

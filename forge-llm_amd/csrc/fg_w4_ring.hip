@@ -482,12 +482,13 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
 }
 
 // CDNA4 layout: 33..64 rows, and 9..32 over K >= 8192; below that the register ring is as fast or faster.
-// portable_row: also 17..32 rows, and 13..16 rows over wide outputs, where the ring replaces the skinny kernel (us,
+// portable_row: also 17..32 rows, and 4..16 rows over wide outputs, where the ring replaces the skinny kernel (us,
 // ring / skinny: M = 32 qkv 13.4 / 14.5, o_proj 11.1 / 12.2, gate+up 31.4 / 44.4; M = 24 gate+up 30.1 / 38.8; M = 16
-// gate+up 23.6 / 25.9, qkv 11.0 / 10.0).
+// gate+up 23.6 / 25.9, qkv 11.0 / 10.0; gate+up M = 12 21.0-23.0 / 24.0, M = 8 22.2 / 23.3, M = 4 22.0 / 23.8,
+// M = 3 level).
 bool w4_ring_preferred(bool portable, int M, int N, int K) {
   if (M > 32 || (M > 8 && K >= 8192)) return true;
-  return portable && (M > 16 || (M > 12 && N >= 16384));
+  return portable && (M > 16 || (M > 3 && N >= 16384));
 }
 
 size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K) {
