@@ -213,14 +213,14 @@ bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int 
 
 // Launch shape, from a sweep of (T, KS) on the Llama-3-8B shapes at M = 1 / 16 / 64 (graph replays over a 1.2 GB
 // weight ring): MB = ceil(M / 16) m-tiles (1, 2 or 4); T = 1 tile per wavefront up to 4096 channels (o_proj, down:
-// 256 channel blocks, one per CU), 2 up to 8192 (qkv), else 4 (gate+up; 2 for 1-4 rows, where the extra tiles only
-// lengthen each wavefront's chain); KS = 4 K slices (2 with 4 tiles), fewer when a slice would be shorter than two
-// steps.  Measured (us): o_proj M=16 7.0 (T1 KS4) against 7.5-16.7 for the others, qkv M=16 8.5 (T2 KS4), gate+up
-// M=16 21.3 (T4 KS2) against 22.0 (T2 KS1) and 25.1 (T4 KS4), down M=16 17.1 (T1 KS4).
+// 256 channel blocks, one per CU), 2 up to 8192 (qkv), else 4 (gate+up); KS = 4 K slices (2 with 4 tiles), fewer
+// when a slice would be shorter than two steps.  Measured (us): o_proj M=16 7.0 (T1 KS4) against 7.5-16.7 for the
+// others, qkv M=16 8.5 (T2 KS4), gate+up M=16 21.3 (T4 KS2) against 22.0 (T2 KS1) and 25.1 (T4 KS4), down M=16 17.1
+// (T1 KS4); gate+up M = 1..4 16.4-17.0 with 4 tiles against 19.4-20.1 with 2.
 void w4_frag_plan(int M, int N, int K, int* mb, int* T, int* KS) {
   const int b = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int nsteps = K / 128;
-  const int t = N <= 4096 ? 1 : (N <= 8192 || M <= 4 ? 2 : 4);
+  const int t = N <= 4096 ? 1 : (N <= 8192 ? 2 : 4);
   int ks = t == 4 ? 2 : 4;
   while (ks > 1 && 2 * ks > nsteps) ks /= 2;
   ks = min(ks, w4_frag_max_threads(b, t) / kWave);
