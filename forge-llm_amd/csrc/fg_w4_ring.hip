@@ -321,7 +321,7 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   // Before each step: this step's loads have landed for every wavefront, every wavefront is done with step i - 1's
   // slot and with the row sums of step i - 2, and step i - 1's row sums are in LDS.  With four wavefronts and 17..64
   // rows the loop is unrolled by S so that every ring slot is a constant offset (no per-step address arithmetic: M = 64
-  // o_proj 14.45 -> 13.5 us, gate+up 37.8 -> 35.5-36.0 on the CDNA4 layout); on eight wavefronts and on 1..16 rows the
+  // o_proj 14.45 -> 13.5 us on the CDNA4 layout, and as much on two-tile wavefronts); on eight wavefronts and on 1..16 rows the
   // unrolled form measured slower (portable qkv M = 64 17.5 -> 18.7, down M = 16 14.9 -> 15.5) and the loop stays rolled.
   if constexpr (BW == 4 && MB >= 2) {
     int i = 0;
@@ -451,8 +451,10 @@ bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, in
 }
 
 // Launch shape, from a sweep of (BW, T, KS) against the register-ring kernel (w4_frag_kernel) on the Llama-3-8B
-// shapes at M = 1 / 16 / 32 / 64 (graph replays over a 1.2 GB weight ring): BW = 4 or 8 wavefronts; T = 2 tiles per
-// wavefront for 33..64 rows over at least 1024 tiles (gate+up: 37.9 us against 43.2 with one), else 1; KS = 1 when the
+// shapes at M = 1 / 16 / 32 / 64 (graph replays over a 1.2 GB weight ring): BW = 4 or 8 wavefronts, one tile each
+// (T = 2 tiles per wavefront on four wavefronts was the gate+up choice before eight wavefronts shared the x row sums;
+// now slower: M = 33 / 64 on the CDNA4 layout 34.7 / 35.9 us against 31.1 / 33.8, W8A16 M = 64 45.8 against 42.2,
+// so the T = 2 instances are not built); KS = 1 when the
 // channel groups fill three quarters of the CUs, else the smallest power of two that gives one wavefront per SIMD,
 // doubled while a split is longer than 16 steps over K >= 8192 (down: 8 splits of 14 steps, 26.0 us at M = 64 against
 // 30.7 with 4).
@@ -467,10 +469,10 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   RingPlan p;
   p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int NT = N / 16, nsteps = K / 128, cus = device_cus();
-  p.T = p.mb == 4 && NT >= 1024 ? 2 : 1;
-  // eight wavefronts (x shared by 128 channels) for 33..64 rows over one-tile wavefronts on qkv-sized or long-K
-  // weights: qkv M = 64 17.1 us against 18.5, down 25.7 against 28.2; o_proj 15.7 against 14.6 stays on four
-  p.BW = p.mb == 4 && p.T == 1 && (NT >= 384 || nsteps >= 64) ? 8 : 4;
+  p.T = 1;
+  // eight wavefronts (x shared by 128 channels) for 33..64 rows on qkv-sized, wide or long-K weights: qkv M = 64
+  // 17.1 us against 18.5, down 25.7 against 28.2; o_proj 15.7 against 14.6 stays on four
+  p.BW = p.mb == 4 && (NT >= 384 || nsteps >= 64) ? 8 : 4;
   p.ngrp = (NT + p.BW * p.T - 1) / (p.BW * p.T);
   int ks = 1;
   if (4 * p.ngrp < 3 * cus)
@@ -530,7 +532,6 @@ template <bool XBF16, bool SBF16, bool PORT>
 static hipError_t launch_ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
   if (p.mb == 1) return launch_ring_t<1, 1, 4, 4, XBF16, SBF16, PORT>(a, s);
   if (p.mb == 2) return launch_ring_t<2, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
-  if (p.T == 2) return launch_ring_t<4, 2, 4, 3, XBF16, SBF16, PORT>(a, s);
   return p.BW == 8 ? launch_ring_t<4, 1, 8, 3, XBF16, SBF16, PORT>(a, s)
                    : launch_ring_t<4, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
 }
@@ -616,7 +617,6 @@ template <bool XBF16, bool SBF16>
 static hipError_t launch_w8ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
   if (p.mb == 1) return launch_w8ring_t<1, 1, 4, 4, XBF16, SBF16>(a, s);
   if (p.mb == 2) return launch_w8ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
-  if (p.T == 2) return launch_w8ring_t<4, 2, 4, 3, XBF16, SBF16>(a, s);
   return p.BW == 8 ? launch_w8ring_t<4, 1, 8, 3, XBF16, SBF16>(a, s) : launch_w8ring_t<4, 1, 4, 3, XBF16, SBF16>(a, s);
 }
 
