@@ -18,9 +18,9 @@
 // Arithmetic, as w4_frag_kernel: B = magic | nibble pair ((word >> 4 p) & 0x000F000F | 0x4300 4300 for bf16, 0x6400
 // 6400 for fp16: the exact values 128 + q / 1024 + q), one v_and_or_b32 per pair (plus a shift for p > 0); per step
 // acc += s * (acc_step - (B + z) * xsum), the x row sums from MFMAs against all-ones.  The row sums of a step are the
-// same for every wavefront: on eight wavefronts, wavefront b < 4 computes those of row block b into an LDS pair buffered
-// by step parity, and every wavefront subtracts s * (B + z) * xsum one step later, after the next step's barrier has
-// made them visible (the last step's after one more barrier at the end).
+// same for every wavefront: on eight wavefronts, wavefront b < MB computes those of row block b into an LDS pair
+// buffered by step parity, and every wavefront subtracts s * (B + z) * xsum one step later, after the next step's
+// barrier has made them visible (the last step's after one more barrier at the end).
 //
 // K splits (KS > 1): each split writes its fp32 partial to the caller's workspace [KS, M, N] and w4_ring_reduce_kernel
 // sums them in split order (bit-reproducible), adds the bias and rounds, eight outputs per thread.  (Letting the last
@@ -83,7 +83,7 @@ struct RingShape {
   static constexpr int SB = W8 ? 256 : 512;   // per wavefront: 256 bytes of scales (+ 256 of zero words for W4)
   static constexpr int SZ = BW * SB;
   static constexpr int STAGE = X + W + SZ;
-  static constexpr bool SHARE = MB == 4 && BW == 8;  // x row sums computed once per workgroup (w4_ring_kernel)
+  static constexpr bool SHARE = MB >= 2 && BW == 8;  // x row sums computed once per workgroup (w4_ring_kernel)
   static constexpr int XS = SHARE ? 2 * MB * 16 * 4 : 0;  // the row sums of two steps (fp32), after the S stages
   static constexpr int XI = 4 * MB / BW;      // x loads (1 KiB = 4 rows each) per wavefront and step
   static constexpr int NI = XI + (W8 ? 2 * T + 1 : T + 2);  // loads per wavefront and step
@@ -125,7 +125,7 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   constexpr bool PORT = FMT != 0, W8 = FMT == 2;
   using Sh = RingShape<MB, T, BW, W8>;
   static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
-  // Row sums shared through LDS on eight wavefronts of 33..64 rows (wavefront b < 4 computes row block b's).  Elsewhere
+  // Row sums shared through LDS on eight wavefronts of 17..64 rows (wavefront b < MB computes row block b's).  Elsewhere
   // every wavefront computes its MB blocks' sums itself: with fewer row blocks than wavefronts wavefront 0 computes as
   // many either way, and on four wavefronts the fewer MFMAs did not make up for the extra LDS reads of x (M = 64:
   // qkv 17.2 -> 16.5 us, down 25.2 -> 23.7 with sharing; o_proj 14.4 -> 14.8, gate+up level on four wavefronts).
@@ -470,9 +470,11 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int NT = N / 16, nsteps = K / 128, cus = device_cus();
   p.T = 1;
-  // eight wavefronts (x shared by 128 channels) for 33..64 rows on qkv-sized, wide or long-K weights: qkv M = 64
-  // 17.1 us against 18.5, down 25.7 against 28.2; o_proj 15.7 against 14.6 stays on four
-  p.BW = p.mb == 4 && (NT >= 384 || nsteps >= 64) ? 8 : 4;
+  // eight wavefronts (x shared by 128 channels, row sums once per workgroup) for 17..64 rows on qkv-sized, wide or
+  // long-K weights: M = 64 qkv 17.1 us against 18.5, down 25.7 against 28.2; M = 17..32 (portable) qkv 11.9-13.0
+  // against 12.3-13.3, gate+up 26.0-26.8 against 27.2-28.3, down 17.2-18.8 against 18.4-20.0, W8A16 down M = 24 19.4
+  // against 23.8; o_proj stays on four (M = 64 15.7 against 14.6, M = 17..32 10.4-11.4 against 10.0-10.6)
+  p.BW = p.mb >= 2 && (NT >= 384 || nsteps >= 64) ? 8 : 4;
   p.ngrp = (NT + p.BW * p.T - 1) / (p.BW * p.T);
   int ks = 1;
   if (4 * p.ngrp < 3 * cus)
@@ -531,7 +533,8 @@ static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
 template <bool XBF16, bool SBF16, bool PORT>
 static hipError_t launch_ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
   if (p.mb == 1) return launch_ring_t<1, 1, 4, 4, XBF16, SBF16, PORT>(a, s);
-  if (p.mb == 2) return launch_ring_t<2, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
+  if (p.mb == 2) return p.BW == 8 ? launch_ring_t<2, 1, 8, 3, XBF16, SBF16, PORT>(a, s)
+                                   : launch_ring_t<2, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
   return p.BW == 8 ? launch_ring_t<4, 1, 8, 3, XBF16, SBF16, PORT>(a, s)
                    : launch_ring_t<4, 1, 4, 3, XBF16, SBF16, PORT>(a, s);
 }
@@ -616,7 +619,8 @@ static hipError_t launch_w8ring_t(const RingArgs& a, hipStream_t s) {
 template <bool XBF16, bool SBF16>
 static hipError_t launch_w8ring_x(const RingPlan& p, const RingArgs& a, hipStream_t s) {
   if (p.mb == 1) return launch_w8ring_t<1, 1, 4, 4, XBF16, SBF16>(a, s);
-  if (p.mb == 2) return launch_w8ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
+  if (p.mb == 2) return p.BW == 8 ? launch_w8ring_t<2, 1, 8, 3, XBF16, SBF16>(a, s)
+                                   : launch_w8ring_t<2, 1, 4, 3, XBF16, SBF16>(a, s);
   return p.BW == 8 ? launch_w8ring_t<4, 1, 8, 3, XBF16, SBF16>(a, s) : launch_w8ring_t<4, 1, 4, 3, XBF16, SBF16>(a, s);
 }
 

@@ -48,11 +48,11 @@ def test_skinny_matches_oracle(m, n, k, gs, xdt):
 
 
 # The LDS-ring kernel through the automatic policy (17..64 rows, and 3..16 over N >= 16384 or K >= 8192), one case per
-# launch shape: one row block (K split 16 ways + reduce / whole K), two, four on four wavefronts, four with two tiles per
-# wavefront, four on eight wavefronts (row sums shared through LDS; wide N / long K), one group per row, bias or not.
+# launch shape: one row block (K split 16 ways + reduce / whole K), two, four on four wavefronts, two and four on eight
+# wavefronts (row sums shared through LDS; wide N / long K), one group per row, bias or not.
 @pytest.mark.parametrize("m,n,k,gs", [(5, 16384, 1024, 128), (12, 1024, 8192, 256), (17, 2048, 2048, -1),
                                       (40, 4096, 4096, 128), (64, 16384, 1024, 128), (33, 6144, 2048, 128),
-                                      (64, 1024, 8192, 128)])
+                                      (64, 1024, 8192, 128), (24, 6144, 1024, 128)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_ring_matches_oracle(m, n, k, gs, xdt):
     sdt = torch.bfloat16 if m % 2 else torch.float16
