@@ -485,13 +485,15 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   return p;
 }
 
-// CDNA4 layout: 33..64 rows, and 9..32 over K >= 8192; below that the register ring is as fast or faster.
+// CDNA4 layout: 29..64 rows, and 9..28 over K >= 8192; below that the register ring is as fast or faster (us, LDS ring /
+// register ring: M = 32 qkv 12.6 / 12.8, o_proj 10.3 / 11.3, gate+up 24.4 / 26.8; M = 24 qkv 12.2 / 11.6, o_proj and
+// gate+up level; M = 17 qkv 11.7 / 10.3, o_proj 9.7 / 8.9).
 // portable_row: also 17..32 rows, and 4..16 rows over wide outputs, where the ring replaces the skinny kernel (us,
 // ring / skinny: M = 32 qkv 13.4 / 14.5, o_proj 11.1 / 12.2, gate+up 31.4 / 44.4; M = 24 gate+up 30.1 / 38.8; M = 16
 // gate+up 23.6 / 25.9, qkv 11.0 / 10.0; gate+up M = 12 21.0-23.0 / 24.0, M = 8 22.2 / 23.3, M = 4 22.0 / 23.8,
 // M = 3 level).
 bool w4_ring_preferred(bool portable, int M, int N, int K) {
-  if (M > 32 || (M > 8 && K >= 8192)) return true;
+  if (M > 28 || (M > 8 && K >= 8192)) return true;
   return portable && (M > 16 || (M > 3 && N >= 16384));
 }
 

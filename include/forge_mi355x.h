@@ -128,7 +128,7 @@ size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
  *   qweight  int32 [ceil(N/16), ldq]: 16-channel tile rows, 256 words per 128-column tile, ldq >= 2 * K (K % 128 == 0)
  *   no perm / g_idx (act-order weights are column-sorted first)
  *   workspace  16-byte aligned, at least fg_w4a16_cdna4_workspace_bytes(M, N, K, group_size) bytes (NULL when that
- *              is 0): fp32 K-split partials of the LDS-ring kernel (33..64 rows, or 9..64 over K >= 8192), summed by a
+ *              is 0): fp32 K-split partials of the LDS-ring kernel (29..64 rows, or 9..64 over K >= 8192), summed by a
  *              second launch in split order; smaller M runs one launch that sums its K slices in LDS
  * Needs group_size % 128 == 0 (or one group), fp16 / bf16 scales, 16-byte aligned x (ldx % 8 == 0) and qweight. */
 int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,

@@ -31,7 +31,7 @@ def _case(m, n, k, gs, sym, xdt, sdt=torch.float16, bias=True, seed=0):
     return y, ref, p
 
 
-@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 33, 48, 64])
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 30, 33, 48, 64])
 @pytest.mark.parametrize("n,k,gs", [(4096, 4096, 128), (1000, 2048, 256), (40, 512, -1)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_cdna4_matches_oracle(m, n, k, gs, xdt):
