@@ -663,11 +663,13 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
              : impl == FG_W4_PREFILL ? 2
              : impl == FG_W4_GEMV  ? 3
                                    : -1;
-  // 1..2 rows: the decode GEMV (graph replays, M = 1, us, GEMV / skinny: qkv 6.2 / 9.6, o_proj 5.1 / 8.0, gate+up
-  // 20.7 / 28.7, down 12.6 / 17.3; M = 4 gate+up 34.4 / 27.7); then the LDS ring (w8a16_ring_rows), else the skinny
-  // kernel up to 64 rows
+  // 1..2 rows, and 3..4 over N <= 8192 and K < 8192: the decode GEMV (graph replays, M = 1, us, GEMV / skinny: qkv
+  // 6.2 / 9.6, o_proj 5.1 / 8.0, gate+up 20.7 / 28.7, down 12.6 / 17.3; M = 3 / 4 o_proj 6.8 / 7.0 against 7.3 / 7.5,
+  // qkv level, gate+up 33.2 against 27.1 on the ring); then the LDS ring (w8a16_ring_rows), else the skinny kernel up
+  // to 64 rows
+  const bool gemv_rows = M <= 2 || (M <= 4 && N <= 8192 && K < 8192);
   if (kern < 0)
-    kern = (gemv && M <= 2) ? 3 : ((ring && w8a16_ring_rows(M, N, K)) ? 4 : ((skinny && M <= 64) ? 1 : (big ? 2 : 0)));
+    kern = (gemv && gemv_rows) ? 3 : ((ring && w8a16_ring_rows(M, N, K)) ? 4 : ((skinny && M <= 64) ? 1 : (big ? 2 : 0)));
   if (kern == 3 && !gemv)
     return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: decode GEMV needs M<=4, K%%16==0, group%%16==0 (or one group), "
                                  "16-bit scales with lds%%8==0, ldq%%16==0, ldx%%8==0, 16-byte aligned x/qweight/"

@@ -155,8 +155,9 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
  *   x        bf16|fp16 [M, K] (row stride ldx)
  *   qweight  int8 [N, K] (row stride ldq, bytes; portable_row PackedW8, forge/kernels/layouts/w8.py:18-104)
  *   scales   fp16|bf16|fp32 [G, N] (row stride lds);  group_size <= 0: one group per row (per-channel)
- *   cfg      NULL (policy: decode GEMV for 1..2 rows; LDS-ring kernel for 17..64 rows and for 3..16 over N >= 16384
- *            or K >= 8192; skinny kernel for the other rows up to 64; then the prefill kernel) or impl FG_W4_GEMV
+ *   cfg      NULL (policy: decode GEMV for 1..2 rows and 3..4 over N <= 8192 and K < 8192; LDS-ring kernel for
+ *            17..64 rows and for 3..16 over N >= 16384 or K >= 8192; skinny kernel for the other rows up to 64;
+ *            then the prefill kernel) or impl FG_W4_GEMV
  *            (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL (dequantise-to-LDS
  *            kernel), FG_W4_GENERIC (any shape); split_k for the prefill kernel
  *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernel or, under the policy, of the
