@@ -125,10 +125,11 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   constexpr bool PORT = FMT != 0, W8 = FMT == 2;
   using Sh = RingShape<MB, T, BW, W8>;
   static_assert(S >= 2 && (S - 2) * Sh::NI <= 63, "the wait count must fit vmcnt");
-  // Row sums shared through LDS on eight wavefronts of 17..64 rows (wavefront b < MB computes row block b's).  Elsewhere
-  // every wavefront computes its MB blocks' sums itself: with fewer row blocks than wavefronts wavefront 0 computes as
-  // many either way, and on four wavefronts the fewer MFMAs did not make up for the extra LDS reads of x (M = 64:
-  // qkv 17.2 -> 16.5 us, down 25.2 -> 23.7 with sharing; o_proj 14.4 -> 14.8, gate+up level on four wavefronts).
+  // Row sums shared through LDS on eight wavefronts of 17..64 rows (wavefront b < MB computes row block b's).
+  // Elsewhere every wavefront computes its MB blocks' sums itself: with fewer row blocks than wavefronts wavefront 0
+  // computes as many either way, and on four wavefronts the fewer MFMAs did not make up for the extra LDS reads of x
+  // (M = 64: qkv 17.2 -> 16.5 us, down 25.2 -> 23.7 with sharing; o_proj 14.4 -> 14.8, gate+up level on four
+  // wavefronts).
   constexpr bool SHARE = Sh::SHARE;
   constexpr float kB = XBF16 ? 128.f : 1024.f;
   constexpr float kCorr8 = XBF16 ? 128.f : 1152.f;  // W8: B = q + 128 (bf16) / 1024 + q + 128 (fp16)
@@ -169,7 +170,7 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
                        ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq + 16u * (uint32_t)unit
                        : a.qbytes;
       }
-    } else if constexpr (PORT) {  // LDS position lane = row lane / 4, slot lane % 4, holding quarter slot ^ (row / 4 % 4)
+    } else if constexpr (PORT) {  // LDS position lane = row lane / 4, slot lane % 4: quarter slot ^ (row / 4 % 4)
       const int row = lane >> 2, quarter = (lane & 3) ^ ((lane >> 4) & 3);
       wv[t][0] = tile0 + t < NT
                      ? ((uint32_t)(tile0 + t) * 16u + (uint32_t)row) * (uint32_t)a.ldq * 4u + 16u * (uint32_t)quarter
@@ -321,8 +322,9 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   // Before each step: this step's loads have landed for every wavefront, every wavefront is done with step i - 1's
   // slot and with the row sums of step i - 2, and step i - 1's row sums are in LDS.  With four wavefronts and 17..64
   // rows the loop is unrolled by S so that every ring slot is a constant offset (no per-step address arithmetic: M = 64
-  // o_proj 14.45 -> 13.5 us on the CDNA4 layout, and as much on two-tile wavefronts); on eight wavefronts and on 1..16 rows the
-  // unrolled form measured slower (portable qkv M = 64 17.5 -> 18.7, down M = 16 14.9 -> 15.5) and the loop stays rolled.
+  // o_proj 14.45 -> 13.5 us on the CDNA4 layout, and as much on two-tile wavefronts); on eight wavefronts and on 1..16
+  // rows the unrolled form measured slower (portable qkv M = 64 17.5 -> 18.7, down M = 16 14.9 -> 15.5) and the loop
+  // stays rolled.
   if constexpr (BW == 4 && MB >= 2) {
     int i = 0;
     for (; i + S <= ns; i += S) {
@@ -485,9 +487,9 @@ static RingPlan w4_ring_plan(int M, int N, int K) {
   return p;
 }
 
-// CDNA4 layout: 29..64 rows, and 9..28 over K >= 8192; below that the register ring is as fast or faster (us, LDS ring /
-// register ring: M = 32 qkv 12.6 / 12.8, o_proj 10.3 / 11.3, gate+up 24.4 / 26.8; M = 24 qkv 12.2 / 11.6, o_proj and
-// gate+up level; M = 17 qkv 11.7 / 10.3, o_proj 9.7 / 8.9).
+// CDNA4 layout: 29..64 rows, and 9..28 over K >= 8192; below that the register ring is as fast or faster (us, LDS
+// ring / register ring: M = 32 qkv 12.6 / 12.8, o_proj 10.3 / 11.3, gate+up 24.4 / 26.8; M = 24 qkv 12.2 / 11.6,
+// o_proj and gate+up level; M = 17 qkv 11.7 / 10.3, o_proj 9.7 / 8.9).
 // portable_row: also 17..32 rows, and 4..16 rows over wide outputs, where the ring replaces the skinny kernel (us,
 // ring / skinny: M = 32 qkv 13.4 / 14.5, o_proj 11.1 / 12.2, gate+up 31.4 / 44.4; M = 24 gate+up 30.1 / 38.8; M = 16
 // gate+up 23.6 / 25.9, qkv 11.0 / 10.0; gate+up M = 12 21.0-23.0 / 24.0, M = 8 22.2 / 23.3, M = 4 22.0 / 23.8,
