@@ -251,8 +251,10 @@ constexpr int64_t kPrefillMinM = 33;
 // dequantisation costs 2.5 N K bytes once, the fused kernel loses a share of every MFMA cycle.  Graph replays over four
 // distinct weights, us, fused / dequantise + GEMM: M = 1024 qkv 87.9 / 72.9, o_proj 65.0 / 56.8, down 177 / 172,
 // gate+up 261 / 278; M = 2048 127 / 104, 93 / 77, 297 / 248, 494 / 438; M = 8192 408 / 310, 282 / 203, 844 / 645,
-// 1711 / 1302; M = 512 fused ahead (down 97 / 133).
-int64_t dequant_gemm_min_m(int64_t N, int64_t K) { return N * K > (64LL << 20) ? 1536 : 1024; }
+// 1711 / 1302.  With the wavefront-per-2048-columns dequantisation the route moved ahead from 768 rows on every shape
+// (M = 768: qkv 86 / 62, o_proj 59 / 46, gate+up 249 / 209, down 153 / 132; gate+up M = 1024 253 / 242); at M = 512
+// the fused kernel stays ahead but for qkv (o_proj 40 / 43, gate+up 141 / 160, down 89 / 113, qkv 60 / 54).
+int64_t dequant_gemm_min_m(int64_t, int64_t) { return 768; }
 
 // Whether the automatic policy sends a 4..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
 // 4..16 over N >= 16384 and 9..16 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring

@@ -39,7 +39,7 @@ enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_
    group % 32 == 0 or one group, aligned x / qweight, no act-order perm)
    FG_W4_DEQUANT_GEMM: the reference's large-M route (forge/kernels/triton/gemm_w4_dequant.py:194-256): the weights
    dequantised once into the workspace, then hipBLASLt's bf16 / fp16 GEMM (fp32 accumulation, bias in its epilogue);
-   the policy takes it from 1024 rows (1536 over weights above 64 Mi elements) when the caller's workspace holds it
+   the policy takes it from 768 rows when the caller's workspace holds it
    (never in fg_w4a16_gemm_noalloc).  Needs
    K % 8 == 0, no act-order perm (a g_idx is fine), a bias in fp32 or x's dtype, a 256-byte aligned workspace. */
 

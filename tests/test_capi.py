@@ -72,19 +72,19 @@ def test_workspace_query_follows_the_kernel_plan(m, n, k, expect_ws):
     L = _lib.lib()
     ws = L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, None)
     assert (ws > 0) == expect_ws
-    if ws and m < 1024:  # split-K partials
+    if ws and m < 768:  # split-K partials
         assert ws % (m * n * 4) == 0 and ws // (m * n * 4) > 1
-    if m >= 1024:  # the dequantise + library GEMM route: the dequantised weights and hipBLASLt's 32 MiB
+    if m >= 768:  # the dequantise + library GEMM route: the dequantised weights and hipBLASLt's 32 MiB
         assert ws >= n * k * 2 + (32 << 20)
         cfg = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
         assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(cfg)) == n * k * 2 + (32 << 20)
     # forcing one split removes the workspace
     cfg = _lib.W4Config(_lib.W4_MFMA, 0, 0, 0, 1)
     assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(cfg)) == 0
-    # the generic kernel never needs one; a g_idx call routes there below 1024 rows (from 1024 the dequantisation
+    # the generic kernel never needs one; a g_idx call routes there below 768 rows (from 768 the dequantisation
     # applies g_idx and the library GEMM follows)
     gidx_ws = L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 1, None)
-    assert gidx_ws == (0 if m < 1024 else n * k * 2 + (32 << 20))
+    assert gidx_ws == (0 if m < 768 else n * k * 2 + (32 << 20))
 
 
 def _header_prototypes() -> dict[str, list[str]]:

@@ -1,6 +1,6 @@
 """GPU parity of W4A16's dequantise + library GEMM route (the reference's large-M route,
 forge/kernels/triton/gemm_w4_dequant.py:194-256): the weights dequantised once into the workspace by the dense
-dequantisation kernel, then hipBLASLt's bf16 / fp16 GEMM with the bias in its epilogue.  The policy takes it from 1024
+dequantisation kernel, then hipBLASLt's bf16 / fp16 GEMM with the bias in its epilogue.  The policy takes it from 768
 rows; forced through config={"impl": "dequant_gemm"} (the reference's "dequant_matmul") at any M.  Cases: bf16 / fp16
 x, bias in x's dtype / fp32 / none, a bias type the route does not take (the fused kernel serves the call), weights
 large enough to go through in two channel chunks, act-order weights (the sorted weight's perm keeps them on the fused
@@ -38,12 +38,13 @@ def _run(m, n, k, xdt, bdt, *, seed, config=None, sym=False):
 
 
 @pytest.mark.parametrize("m,kn,xdt,bdt", [
+    (768, (4096, 28672), torch.bfloat16, torch.bfloat16),
     (1024, (4096, 6144), torch.bfloat16, torch.bfloat16),
     (1500, (4096, 6144), torch.float16, torch.float32),
     (1024, (14336, 4096), torch.bfloat16, None),
     (2048, (4096, 4096), torch.float16, torch.float16),
 ])
-def test_policy_takes_the_route_from_1024_rows(m, kn, xdt, bdt):
+def test_policy_takes_the_route_from_768_rows(m, kn, xdt, bdt):
     k, n = kn
     y, ref, (x, p, bd) = _run(m, n, k, xdt, bdt, seed=m + n)
     assert_close(y.cpu(), ref, ODT[xdt], what=f"dequant+gemm m={m} k={k} n={n}")
