@@ -1113,8 +1113,9 @@ hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales,
                              const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int odt, int64_t ldo,
                              int N, int K, int gs, hipStream_t s) {
   const bool one_group = gs >= K;
+  // K < 2^27: the multiply-high group division below is exact for column indices times the group size under 2^32
   if (!g_idx && (odt == FG_BF16 || odt == FG_F16) && (sdt == FG_BF16 || sdt == FG_F16) && K % 32 == 0 &&
-      (gs % 32 == 0 || one_group) && reinterpret_cast<uintptr_t>(qw) % 4 == 0 && ldo % 8 == 0 &&
+      K < (1 << 27) && (gs % 32 == 0 || one_group) && reinterpret_cast<uintptr_t>(qw) % 4 == 0 && ldo % 8 == 0 &&
       reinterpret_cast<uintptr_t>(out) % 16 == 0) {
     const int wpr = (K + 2047) / 2048;  // wavefronts per channel row
     const int64_t blocks = ((int64_t)N * wpr + 3) / 4;
