@@ -198,17 +198,21 @@ int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t l
     //    60 for the ring kernel); at K = 8192 the ring kernel is ahead from M = 1 (int8 N=10240: 20 against 27; fp8
     //    N=8192 at M=16: 17 against 19; int8 N=57344: 96 against 112), and at M = 32..64 everywhere (int8 K=28672,
     //    M=64: 63 against 139);
-    //  * the 256-row kernel once its tiles cover the CUs, and from 5/8 of the CUs' worth with M >= 1024 (int8 M=1024,
-    //    K=8192, N=10240: 160 tiles, 113 against 130 for 128-row ring tiles; at 128 tiles the ring is ahead: fp8
-    //    M=1024, K=N=8192, 89 against 117, int8 K=28672, N=8192, 297 against 353);
+    //  * the 256-row kernel once its tiles number 5/8 of the CUs, whatever M (int8 M=1024, K=8192, N=10240: 160 tiles,
+    //    113 against 130 for 128-row ring tiles; K=8192, M=160..224, N=57344: 224 tiles, 146-150 against 180-186
+    //    int8 and 150-156 against 168-180 fp8; M=300..448, N=28672: 118-128 against 131-177; M=640, N=14336: 168
+    //    tiles, 102 against 120); at 112-128 tiles the ring is ahead (fp8 M=1024, K=N=8192, 89 against 117; int8
+    //    K=28672, N=8192, 297 against 353; K=8192, N=28672, M=160..224, 110-124 against 88-96);
     //  * below that the ring kernel: 128-row tiles once they number 5/8 of the CUs (fp8 M=512: 256 tiles, 47 against
-    //    62 for 64 x 128), else 64-row tiles (fp8 M=256: 33 against 65 for the register-staged 64 x 64 tiles).
+    //    62 for 64 x 128) unless 64 x 128 tiles fit one per CU (int8 K=8192, N=10240, M=160..192: 240 tiles, 34-35
+    //    against 41; M=224: 320 tiles, 57 against 43), else 64-row tiles (fp8 M=256: 33 against 65 for the
+    //    register-staged 64 x 64 tiles).
     if (skinny_ok && M <= 16 && K >= 16384) return 16;
     const int64_t tiles = fg::mm_big_tiles(M, N), cus = fg::device_cus();
-    if (tiles >= cus || (M >= 1024 && 8 * tiles >= 5 * cus)) return 256;
+    if (8 * tiles >= 5 * cus) return 256;
     *ring = true;
-    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-    return (M > 64 && 8 * t128 >= 5 * cus) ? 128 : 64;
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128), t64 = ((M + 63) / 64) * ((N + 127) / 128);
+    return (M > 64 && 8 * t128 >= 5 * cus && t64 > cus) ? 128 : 64;
   }
   // Unaligned operands or K % 128 != 0: the skinny kernel where it applies and was measured faster, else the
   // register-staged tiles (64-row while 128-row tiles would leave fewer than two per CU).

@@ -121,5 +121,35 @@ def test_big_fp8_full_size_matches_128_tiles():
     assert_close(y[rows].cpu(), ref, "bfloat16", what="fp8 full-size rows")
 
 
+@pytest.mark.parametrize("m,n,cfg", [(192, 57344, BIG), (300, 28672, BIG), (640, 14336, BIG),
+                                     (160, 10240, {"tile_m": 64, "tile_n": 128})])
+def test_policy_mid_m_kernels(m, n, cfg):
+    """129..1023 rows: the 256-row kernel once its tiles number 5/8 of the CUs (224 tiles at M = 192 / 300, 168 at
+    M = 640) and 64 x 128 ring tiles where they fit one per CU (240 at M = 160, N = 10240).  The policy's INT8 and FP8
+    results equal the named instance's bit for bit and match the oracle on sampled rows (bf16 output, per-token x
+    per-channel scales, bias)."""
+    k = 512
+    g = torch.Generator(device=DEV).manual_seed(m + n)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=DEV, generator=g)
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=DEV, generator=g)
+    sa = torch.rand(m, device=DEV, generator=g) * 0.01 + 0.001
+    sw = torch.rand(n, device=DEV, generator=g) * 0.01 + 0.001
+    b = torch.randn(n, device=DEV, generator=g)
+    y = ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16)
+    assert torch.equal(y, ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16, config=cfg))
+    rows = sorted({0, m // 2, m - 1})
+    xq, wq = a[rows].cpu().numpy(), w.cpu().numpy()
+    ref = og.int8_gemm_ref(xq, sa[rows].cpu().numpy(), wq, sw.cpu().numpy(), b.cpu().numpy(),
+                           acc=og.int8_matmul_exact(xq, wq))
+    assert torch.equal(y[rows].cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+    x = torch.randn(m, k, device=DEV, generator=g).bfloat16()
+    xf, sx = ops.quantize_act_fp8(x)
+    wf, swf = ops.quantize_weight_fp8(torch.randn(n, k, device=DEV, generator=g) * 0.02, "per_channel")
+    yf = ops.fp8_linear(xf, wf, swf, x_scale=sx, out_dtype=torch.bfloat16)
+    assert torch.equal(yf, ops.fp8_linear(xf, wf, swf, x_scale=sx, out_dtype=torch.bfloat16, config=cfg))
+    ref = og.fp8_gemm_ref(ops_codes(xf[rows]), sx[rows].cpu().numpy(), ops_codes(wf), swf.cpu().numpy())
+    assert_close(yf[rows].cpu(), ref, "bfloat16", what=f"fp8 policy m={m} n={n}")
+
+
 def ops_codes(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().view(torch.uint8).numpy()
