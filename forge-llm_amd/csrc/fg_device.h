@@ -83,6 +83,14 @@ struct FastDiv {
   __device__ __forceinline__ uint32_t div(uint32_t n) const { return d > 1 ? __umulhi(n, m) : n; }
 };
 
+// Whether a kernel's group index, the chunk index (chunks of `unit` columns below K) divided by the chunks per group
+// with one multiply-high (FastDiv, or the same m inline), is exact for every chunk: one group, a power-of-two group
+// (m = 2^32 / d exactly), or (K / unit) * (gs / unit) < 2^32.
+inline bool group_div_exact(int64_t K, int64_t gs, int64_t G, int64_t unit) {
+  const int64_t d = gs / unit, c = (K + unit - 1) / unit;
+  return G == 1 || d <= 1 || (d & (d - 1)) == 0 || c * d < (1LL << 32);
+}
+
 // Value of lane l ^ o (o = 1, 2) or of a partner in the other o-half of its 8/16-lane group (o = 4: mirror within 8
 // lanes, o = 8: rotate by 8 within 16 lanes) through DPP, without LDS traffic.
 template <int O>

@@ -1113,14 +1113,14 @@ hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales,
                              const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int odt, int64_t ldo,
                              int N, int K, int gs, hipStream_t s) {
   const bool one_group = gs >= K;
-  // K < 2^27: the multiply-high group division below is exact for column indices times the group size under 2^32
   if (!g_idx && (odt == FG_BF16 || odt == FG_F16) && (sdt == FG_BF16 || sdt == FG_F16) && K % 32 == 0 &&
-      K < (1 << 27) && (gs % 32 == 0 || one_group) && reinterpret_cast<uintptr_t>(qw) % 4 == 0 && ldo % 8 == 0 &&
+      group_div_exact(K, gs, one_group ? 1 : 2, 1) && (gs % 32 == 0 || one_group) &&
+      reinterpret_cast<uintptr_t>(qw) % 4 == 0 && ldo % 8 == 0 &&
       reinterpret_cast<uintptr_t>(out) % 16 == 0) {
     const int wpr = (K + 2047) / 2048;  // wavefronts per channel row
     const int64_t blocks = ((int64_t)N * wpr + 3) / 4;
     const uint32_t gdiv = one_group ? 0u : (uint32_t)gs;
-    const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;  // c / gs = umulhi(c, gmul), c < 2^31
+    const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;  // c / gs = umulhi(c, gmul)
     auto kern = odt == FG_BF16 ? w4_dequant16_kernel<true> : w4_dequant16_kernel<false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, static_cast<const uint16_t*>(scales),
                        (int)(sdt == FG_BF16), lds, zeros, ldz, static_cast<uint16_t*>(out), ldo, N, K, wpr, gdiv, gmul);

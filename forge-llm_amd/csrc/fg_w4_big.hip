@@ -353,7 +353,8 @@ __global__ void __launch_bounds__(kW4BigThreads) w4_big_kernel(
 bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
                int64_t G) {
   return perm == nullptr && (K % kW4BigBK) == 0 && ((gs % 32) == 0 || G == 1) && (ldx % 8) == 0 &&
-         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0;
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0 &&
+         group_div_exact(K, gs, G, 32);
 }
 
 // Row tile and K splits: 256 x 256 tiles when they alone cover the CUs, 64 x 256 for M <= 64, else 128 x 256, split
@@ -445,7 +446,8 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
 // W8A16 through the same kernel (int8 qweight, ldq in bytes, no zero-points).
 bool w8_big_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int64_t K, int gs, int64_t G) {
   return (K % kW4BigBK) == 0 && ((gs % 32) == 0 || G == 1) && (ldx % 8) == 0 &&
-         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0;
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 && (reinterpret_cast<uintptr_t>(qw) % 16) == 0 &&
+         group_div_exact(K, gs, G, 32);
 }
 
 hipError_t launch_w8_big(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq, const void* scales,

@@ -208,7 +208,7 @@ bool w4_frag_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, int 
   return M > 0 && M <= 64 && sdt != FG_F32 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) && (ldx % 8) == 0 &&
          (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 && ldq >= 2 * K &&
          (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && nt * ldq * 4 < k4g && (int64_t)M * ldx * 2 < k4g &&
-         G * lds * 2 < k4g && G * ldz * 4 < k4g;
+         G * lds * 2 < k4g && G * ldz * 4 < k4g && group_div_exact(K, gs, G, 128);
 }
 
 // Launch shape, from a sweep of (T, KS) on the Llama-3-8B shapes at M = 1 / 16 / 64 (graph replays over a 1.2 GB

@@ -449,7 +449,8 @@ bool w4_ring_ok(bool portable, const void* x, int64_t ldx, const int32_t* qw, in
          (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 &&
          ldq >= (portable ? K / 8 : 2 * K) && (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
          (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && (reinterpret_cast<uintptr_t>(zeros) % 4) == 0 &&
-         qspan < k2g && (int64_t)M * ldx * 2 < k2g && G * lds * 2 < k2g && G * ldz * 4 < k2g;
+         qspan < k2g && (int64_t)M * ldx * 2 < k2g && G * lds * 2 < k2g && G * ldz * 4 < k2g &&
+         group_div_exact(K, gs, G, 128);
 }
 
 // Launch shape, from a sweep of (BW, T, KS) against the register-ring kernel (w4_frag_kernel) on the Llama-3-8B
@@ -597,7 +598,8 @@ bool w8a16_ring_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, co
   return M > 0 && M <= 64 && sdt != FG_F32 && N % 16 == 0 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) &&
          (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 16) == 0 && ldq >= K &&
          (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && (lds % 2) == 0 &&
-         (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && N * ldq < k2g && M * ldx * 2 < k2g && G * lds * 2 < k2g;
+         (reinterpret_cast<uintptr_t>(scales) % 4) == 0 && N * ldq < k2g && M * ldx * 2 < k2g && G * lds * 2 < k2g &&
+         group_div_exact(K, gs, G, 128);
 }
 
 size_t w8a16_ring_workspace_bytes(int M, int N, int K) {

@@ -218,7 +218,8 @@ bool w4_skinny_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, co
   return M > 0 && M <= 64 && perm == nullptr && sdt != FG_F32 && (K % 128) == 0 && ((gs % 128) == 0 || G == 1) &&
          (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (ldq % 4) == 0 &&
          (reinterpret_cast<uintptr_t>(qw) % 16) == 0 && N * ldq * 4 < k4g && (int64_t)M * ldx * 2 < k4g &&
-         G * lds * 2 < k4g && G * ldz * 4 < k4g;  // scale / zero buffer spans in bytes
+         G * lds * 2 < k4g && G * ldz * 4 < k4g &&  // scale / zero buffer spans in bytes
+         group_div_exact(K, gs, G, 128);
 }
 
 // Launch shape, from a sweep over the Llama-3-8B shapes at M = 8..64: T tiles of 16 channels per wavefront, the largest
