@@ -2,6 +2,7 @@
 // Declarations and the reference interface each one replaces: include/forge_mi355x.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -79,13 +80,17 @@ bool int8_gemv_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_
 hipError_t launch_int8_gemv(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
                             int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
-size_t w4_libgemm_workspace_bytes(int N, int K);
-bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
+size_t libgemm_workspace_bytes(int N, int K);
+bool libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
                    hipStream_t s);
 hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
                              int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
                              const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
                              void* ws, size_t ws_bytes, hipStream_t s);
+bool w8_dequant16_ok(const int8_t* qw, int64_t ldq, int odt, int64_t K, int gs, int64_t G);
+hipError_t launch_w8a16_libgemm(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq, const void* scales,
+                                int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                                int K, int gs, void* ws, size_t ws_bytes, hipStream_t s);
 size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K);
 hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
                           const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias,
@@ -260,6 +265,13 @@ constexpr int64_t kPrefillMinM = 33;
 // the fused kernel stays ahead but for qkv (o_proj 40 / 43, gate+up 141 / 160, down 89 / 113, qkv 60 / 54).
 int64_t dequant_gemm_min_m(int64_t, int64_t) { return 768; }
 
+// W8A16 rows from which the policy takes the same route (int8 weights dequantised by w8_dequant16_kernel, 3 N K bytes)
+// over the fused prefill kernel.  Graph replays over four distinct weights, us, fused / route: M = 768 qkv 86.9 / 62.4,
+// o_proj 63.1 / 44.8, gate+up 251 / 210, down 179 / 130; M = 2048 124 / 97, 97 / 72, 498 / 409, 317 / 224; M = 8192
+// 415 / 300, 280 / 194, 1807 / 1286, 907 / 640; at M = 512 the fused kernel stays ahead on gate+up (141 / 155) and
+// down (111 / 120).
+int64_t w8a16_dequant_gemm_min_m(int64_t, int64_t) { return 768; }
+
 // Whether the automatic policy sends a 4..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
 // 4..16 over N >= 16384 and 9..16 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
 // / previous choice: M = 64 qkv 17.8 / 22.4, o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 32
@@ -329,7 +341,7 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
                        !(cfg && (cfg->tile_m || cfg->split_k));
   if (use == FG_W4_DEQUANT_GEMM || dq_auto) {
     p->dequant_gemm = true;
-    p->ws_bytes = fg::w4_libgemm_workspace_bytes((int)N, (int)K);
+    p->ws_bytes = fg::libgemm_workspace_bytes((int)N, (int)K);
     if (use == FG_W4_DEQUANT_GEMM) return FG_OK;
   }
   if (use == FG_W4_GEMV) {
@@ -415,7 +427,7 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
   if (p.dequant_gemm) {
-    const bool fits = perm == nullptr && fg::w4_libgemm_ok(x_dtype, bias, bias_dtype, M, N, K, ldx, ldy, s) &&
+    const bool fits = perm == nullptr && fg::libgemm_ok(x_dtype, bias, bias_dtype, M, N, K, ldx, ldy, s) &&
                       reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
     if (fits)
       return hip_status(fg::launch_w4_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
@@ -630,12 +642,20 @@ size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   const int gs = group_size > 0 ? group_size : (int)K;
   const int64_t G = (K + gs - 1) / gs;
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
+  // the dequantise + library GEMM route: forced, or many rows under the policy (the launch falls back to the kernels
+  // below when the operands do not allow the route, so the workspace covers those too)
+  const bool route_shape = K % 16 == 0 && (gs % 16 == 0 || G == 1) && fg::group_div_exact(K, gs, G, 1);
+  if (impl == FG_W4_DEQUANT_GEMM) return route_shape ? fg::libgemm_workspace_bytes((int)N, (int)K) : 0;
+  const size_t route = impl == FG_W4_AUTO && route_shape && M >= w8a16_dequant_gemm_min_m(N, K) &&
+                               !(cfg && (cfg->tile_m || cfg->split_k))
+                           ? fg::libgemm_workspace_bytes((int)N, (int)K)
+                           : 0;
   // the prefill kernel's split-K partials, whenever it may run (its alignment conditions are checked at launch)
   const bool prefill_shape = (K % 64 == 0) && (gs % 32 == 0 || G == 1);
-  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return 0;
+  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return route;
   const size_t ring = impl == FG_W4_AUTO && w8a16_ring_rows(M, N, K) ? fg::w8a16_ring_workspace_bytes((int)M, (int)N, (int)K)
                                                                : 0;
-  return std::max(ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0));
+  return std::max({route, ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0)});
 }
 
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
@@ -656,10 +676,29 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     return fail(FG_EINVAL, "fg_w8a16_gemm: n_groups=%d does not cover K=%lld with group %d", n_groups, (long long)K, gs);
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
   if (impl != FG_W4_AUTO && impl != FG_W4_GEMV && impl != FG_W4_MFMA && impl != FG_W4_PREFILL &&
-      impl != FG_W4_GENERIC)
+      impl != FG_W4_GENERIC && impl != FG_W4_DEQUANT_GEMM)
     return fail(FG_EINVAL, "fg_w8a16_gemm: unknown impl %d", impl);
   const bool xbf16 = x_dtype == FG_BF16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // many rows: dequantise + hipBLASLt's GEMM where the operands, the workspace and (under capture) an existing plan
+  // allow it; forced, it must apply
+  const bool route_auto = impl == FG_W4_AUTO && M >= w8a16_dequant_gemm_min_m(N, K) && !(cfg && (cfg->tile_m || cfg->split_k));
+  if (route_auto || impl == FG_W4_DEQUANT_GEMM) {
+    const bool fits = fg::w8_dequant16_ok(qweight, ldq, x_dtype, K, gs, G) &&
+                      fg::libgemm_ok(x_dtype, bias, bias_dtype, M, N, K, ldx, ldy, s) && workspace &&
+                      reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
+                      workspace_bytes >= fg::libgemm_workspace_bytes((int)N, (int)K);
+    if (fits)
+      return hip_status(fg::launch_w8a16_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, bias,
+                                                 bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, workspace,
+                                                 workspace_bytes, s),
+                        "fg_w8a16_gemm dequantise + library GEMM");
+    if (impl == FG_W4_DEQUANT_GEMM)
+      return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: the dequantise + library GEMM route needs K %% 16 == 0, group %% 16 "
+                                   "== 0 (or one group), ldq %% 16 == 0, 16-byte aligned qweight, a bias in fp32 or x's "
+                                   "dtype, a 256-byte aligned workspace of fg_w8a16_workspace_bytes and, under graph "
+                                   "capture, a first call of the same problem outside it");
+  }
   const bool gemv = fg::w8a16_gemv_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);
   const bool big = fg::w8_big_ok(x, ldx, qweight, ldq, K, gs, G);

@@ -1,10 +1,11 @@
-// W4A16 for many rows of x along the reference's own large-M route (forge/kernels/triton/gemm_w4_dequant.py:194-256,
+// W4A16 (and W8A16) for many rows of x along the reference's own large-M route (forge/kernels/triton/gemm_w4_dequant.py:194-256,
 // chosen by forge/kernels/w4_tuning.py:22-28 from 64 rows): the weights are dequantised once into the caller's
 // workspace by the dense dequantisation kernel -- (q - z) * s in fp32, rounded once to x's dtype, the value the fused
 // prefill kernel stores into LDS -- and then multiplied by hipBLASLt's bf16 / fp16 GEMM (fp32 accumulation, the bias
 // added in fp32 by its epilogue before the single rounding of the output).  A plain library GEMM is what the matrix
-// cores run best from M ~ 1024: the dequantisation costs 2.5 N K bytes of traffic once per call, the GEMM then has no
-// unpack in its loop.  Weights larger than kChunkBytes once dequantised go through in channel chunks.
+// cores run best from M ~ 1024: the dequantisation costs 2.5 N K bytes of traffic once per call (3 N K for int8
+// weights, q * s rounded once, the value the W8A16 prefill kernel stores into LDS), the GEMM then has no unpack in its
+// loop.  Weights larger than kChunkBytes once dequantised go through in channel chunks.
 //
 // Row-major y[M, N] = x[M, K] W[N, K]^T is, column-major, Y^T (N x M, ld ldy) = op(W^T) op(x^T): A = the dequantised
 // W (K x N, ld K) transposed, B = x^T (K x M, ld ldx), D = Y^T.
@@ -26,6 +27,8 @@ namespace fg {
 hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
                              const int32_t* zeros, int64_t ldz, const int32_t* g_idx, void* out, int odt, int64_t ldo,
                              int N, int K, int gs, hipStream_t s);
+hipError_t launch_w8_dequant16(const int8_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds, void* out,
+                               int odt, int64_t ldo, int N, int K, int gs, hipStream_t s);
 
 namespace {
 
@@ -108,7 +111,7 @@ const Plan* get_plan(const PlanKey& k, hipblasLtHandle_t h) {
 
 // Workspace of the dequantise + library GEMM route: one chunk of dequantised weights (16-bit, 256-byte aligned) and
 // hipBLASLt's workspace after it.
-size_t w4_libgemm_workspace_bytes(int N, int K) {
+size_t libgemm_workspace_bytes(int N, int K) {
   const size_t deq = ((size_t)chunk_rows(N, K) * (size_t)K * 2 + 255) / 256 * 256;
   return deq + kLtWorkspace;
 }
@@ -116,7 +119,7 @@ size_t w4_libgemm_workspace_bytes(int N, int K) {
 // Whether the route applies to these operands: 16-bit x, a bias (if any) in fp32 or x's dtype, and a K hipBLASLt
 // reads with 16-byte rows.  Under graph capture only a problem whose handle and plan already exist takes it (creating
 // them may allocate or synchronise, which a capture forbids); the caller's fused kernel serves the rest.
-bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
+bool libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
                    hipStream_t s) {
   if (!((xdt == FG_BF16 || xdt == FG_F16) && (!bias || bdt == FG_F32 || bdt == xdt) && K % 8 == 0)) return false;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -135,23 +138,24 @@ bool w4_libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int
   return true;
 }
 
-hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
-                             int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
-                             const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
-                             void* ws, size_t ws_bytes, hipStream_t s) {
-  if (ws_bytes < w4_libgemm_workspace_bytes(N, K) || reinterpret_cast<uintptr_t>(ws) % 256) return hipErrorInvalidValue;
+namespace {
+
+// Dequantise channel chunk after channel chunk into the workspace (deq(n0, nc, out, stream) writes a 16-bit [nc, K]
+// matrix) and multiply each by x with hipBLASLt.
+template <class Deq>
+hipError_t libgemm_run(const void* x, int64_t ldx, int xdt, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                       int K, void* ws, size_t ws_bytes, hipStream_t s, Deq deq) {
+  if (ws_bytes < libgemm_workspace_bytes(N, K) || reinterpret_cast<uintptr_t>(ws) % 256) return hipErrorInvalidValue;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kLibMaxDevices) return hipErrorInvalidDevice;
   const int rows = chunk_rows(N, K);
-  uint8_t* deq = static_cast<uint8_t*>(ws);
-  uint8_t* ltws = deq + (w4_libgemm_workspace_bytes(N, K) - kLtWorkspace);
-  const size_t esz = sdt == FG_F32 ? 4 : 2;
+  uint8_t* dq = static_cast<uint8_t*>(ws);
+  uint8_t* ltws = dq + (libgemm_workspace_bytes(N, K) - kLtWorkspace);
   for (int n0 = 0; n0 < N; n0 += rows) {
     const int nc = N - n0 < rows ? N - n0 : rows;
-    e = launch_w4_dequant(qw + (int64_t)n0 * ldq, ldq, static_cast<const uint8_t*>(scales) + (size_t)n0 * esz, sdt,
-                          lds, zeros ? zeros + n0 / 8 : nullptr, ldz, g_idx, deq, xdt, K, nc, K, gs, s);
+    e = deq(n0, nc, dq, s);
     if (e != hipSuccess) return e;
     const Plan* p;
     hipblasLtHandle_t h;
@@ -175,11 +179,40 @@ hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t*
     }
     const float alpha = 1.f, beta = 0.f;
     void* yc = static_cast<uint8_t*>(y) + (size_t)n0 * 2;
-    if (hipblasLtMatmul(h, p->desc, &alpha, deq, p->a, x, p->b, &beta, yc, p->d, yc, p->d, &p->algo, ltws, p->ws, s) !=
+    if (hipblasLtMatmul(h, p->desc, &alpha, dq, p->a, x, p->b, &beta, yc, p->d, yc, p->d, &p->algo, ltws, p->ws, s) !=
         HIPBLAS_STATUS_SUCCESS)
       return hipErrorLaunchFailure;
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
+                             int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
+                             const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
+                             void* ws, size_t ws_bytes, hipStream_t s) {
+  const size_t esz = sdt == FG_F32 ? 4 : 2;
+  return libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
+                     [&](int n0, int nc, void* out, hipStream_t st) {
+                       return launch_w4_dequant(qw + (int64_t)n0 * ldq, ldq,
+                                                static_cast<const uint8_t*>(scales) + (size_t)n0 * esz, sdt, lds,
+                                                zeros ? zeros + n0 / 8 : nullptr, ldz, g_idx, out, xdt, K, nc, K, gs,
+                                                st);
+                     });
+}
+
+// W8A16: symmetric int8 weights [N, ldq] with scales [G, lds] (w8_dequant16_ok must hold).
+hipError_t launch_w8a16_libgemm(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq, const void* scales,
+                                int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
+                                int K, int gs, void* ws, size_t ws_bytes, hipStream_t s) {
+  const size_t esz = sdt == FG_F32 ? 4 : 2;
+  return libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
+                     [&](int n0, int nc, void* out, hipStream_t st) {
+                       return launch_w8_dequant16(qw + (int64_t)n0 * ldq, ldq,
+                                                  static_cast<const uint8_t*>(scales) + (size_t)n0 * esz, sdt, lds, out,
+                                                  xdt, K, nc, K, gs, st);
+                     });
 }
 
 }  // namespace fg

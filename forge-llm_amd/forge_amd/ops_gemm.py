@@ -421,9 +421,10 @@ def w4_dequant(packed: PackedW4, dtype: torch.dtype = torch.float32) -> torch.Te
 def w8a16_linear(x: torch.Tensor, packed: PackedW8, bias: torch.Tensor | None = None, *,
                  config: dict[str, Any] | None = None, deterministic: bool = True) -> torch.Tensor:
     """``y = x @ (q * s)^T (+ bias)`` with symmetric int8 weights (``forge/kernels/ops_gemm.py:320-346``) for bf16 /
-    fp16 ``x [..., K]``; returns ``x.dtype``.  A split-K GEMV for 1..4 rows, the skinny MFMA kernel up to 64 rows,
-    dequantise-to-LDS MFMA tiles beyond, a generic kernel for shapes none of them takes (``config={"impl": "gemv" |
-    "mfma" | "prefill" | "generic"}`` overrides); fixed-order reductions throughout."""
+    fp16 ``x [..., K]``; returns ``x.dtype``.  A split-K GEMV for 1..4 rows, the LDS-ring and skinny MFMA kernels up
+    to 64 rows, dequantise-to-LDS MFMA tiles beyond, from 768 rows the weights dequantised once into the workspace and
+    hipBLASLt's GEMM, a generic kernel for shapes none of them takes (``config={"impl": "gemv" | "mfma" | "prefill" |
+    "dequant_gemm" | "generic"}`` overrides); fixed-order reductions throughout."""
     _on_gpu(x, "w8a16_linear")
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise HardwareUnsupported(f"w8a16_linear: activations must be bf16 or fp16, got {x.dtype}")

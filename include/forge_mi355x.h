@@ -157,11 +157,16 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
  *   scales   fp16|bf16|fp32 [G, N] (row stride lds);  group_size <= 0: one group per row (per-channel)
  *   cfg      NULL (policy: decode GEMV for 1..2 rows and 3..4 over N <= 8192 and K < 8192; LDS-ring kernel for
  *            17..64 rows and for 3..16 over N >= 16384 or K >= 8192; skinny kernel for the other rows up to 64;
- *            then the prefill kernel) or impl FG_W4_GEMV
- *            (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL (dequantise-to-LDS
- *            kernel), FG_W4_GENERIC (any shape); split_k for the prefill kernel
+ *            then the prefill kernel; from 768 rows the dequantise + library GEMM route where it applies) or impl
+ *            FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL
+ *            (dequantise-to-LDS kernel), FG_W4_GENERIC (any shape), FG_W4_DEQUANT_GEMM (q * s rounded once to x's
+ *            dtype into the workspace, then hipBLASLt's GEMM with the bias in its epilogue; needs K % 16 == 0,
+ *            group % 16 == 0 or one group, ldq % 16 == 0, 16-byte aligned qweight, a bias in fp32 or x's dtype, a
+ *            256-byte aligned workspace and, under graph capture, a first call of the same problem outside it);
+ *            split_k for the prefill kernel
  *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernel or, under the policy, of the
- *              LDS-ring kernel; 0 when neither splits K)
+ *              LDS-ring kernel, and from 768 rows the route's dequantised weights plus 32 MiB for hipBLASLt; 0 when
+ *              none applies)
  * ------------------------------------------------------------------------------------------------------------- */
 size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, const fg_w4_config* cfg);
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,

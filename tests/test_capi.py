@@ -87,6 +87,19 @@ def test_workspace_query_follows_the_kernel_plan(m, n, k, expect_ws):
     assert gidx_ws == (0 if m < 768 else n * k * 2 + (32 << 20))
 
 
+@pytest.mark.parametrize("m", [768, 4096])
+def test_w8a16_workspace_covers_the_library_route(m):
+    """From 768 rows the W8A16 policy may take the dequantise + library GEMM route: the workspace holds the 16-bit
+    weights and hipBLASLt's 32 MiB; forced, exactly that; a K the dequantisation does not take, none."""
+    L = _lib.lib()
+    n, k, route = 4096, 4096, 4096 * 4096 * 2 + (32 << 20)
+    assert L.fg_w8a16_workspace_bytes(m, n, k, -1, None) >= route
+    cfg = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
+    assert L.fg_w8a16_workspace_bytes(m, n, k, -1, ctypes.byref(cfg)) == route
+    assert L.fg_w8a16_workspace_bytes(m, n, 4104, -1, ctypes.byref(cfg)) == 0
+    assert L.fg_w8a16_workspace_bytes(4, n, k, -1, ctypes.byref(cfg)) == route
+
+
 def _header_prototypes() -> dict[str, list[str]]:
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     protos = {}
