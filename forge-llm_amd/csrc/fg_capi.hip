@@ -81,8 +81,8 @@ hipError_t launch_int8_gemv(const int8_t* a, int64_t lda, const float* sa, int64
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
                             int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
 size_t libgemm_workspace_bytes(int N, int K);
-bool libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
-                   hipStream_t s);
+bool libgemm_ok(int xdt, const void* x, const void* bias, int bdt, const void* y, int64_t M, int64_t N, int64_t K,
+                int64_t ldx, int64_t ldy, hipStream_t s);
 hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
                              int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
                              const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
@@ -427,7 +427,7 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
   if (p.dequant_gemm) {
-    const bool fits = perm == nullptr && fg::libgemm_ok(x_dtype, bias, bias_dtype, M, N, K, ldx, ldy, s) &&
+    const bool fits = perm == nullptr && fg::libgemm_ok(x_dtype, x, bias, bias_dtype, y, M, N, K, ldx, ldy, s) &&
                       reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
     if (fits)
       return hip_status(fg::launch_w4_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
@@ -435,9 +435,9 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
                                               workspace_bytes, s),
                         "fg_w4a16_gemm dequantise + library GEMM");
     if (p.impl == FG_W4_DEQUANT_GEMM)
-      return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs no act-order perm, a bias "
-                                   "in fp32 or x's dtype, a 256-byte aligned workspace and, under graph capture, a "
-                                   "first call of the same problem outside it");
+      return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs no act-order perm, x and "
+                                   "y with 16-byte aligned rows, a bias in fp32 or x's dtype, a 256-byte aligned "
+                                   "workspace and, under graph capture, a first call of the same problem outside it");
   }
   // 3-4 rows over weights larger than 4096 x 4096: the skinny MFMA kernel where it applies (it needs no workspace).
   // Measured at M = 4 (us): qkv 8.2 against 8.7 for the GEMV, gate+up 20.5 against 22.8, down 14.8 against 16.2;
@@ -685,7 +685,7 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
   const bool route_auto = impl == FG_W4_AUTO && M >= w8a16_dequant_gemm_min_m(N, K) && !(cfg && (cfg->tile_m || cfg->split_k));
   if (route_auto || impl == FG_W4_DEQUANT_GEMM) {
     const bool fits = fg::w8_dequant16_ok(qweight, ldq, x_dtype, K, gs, G) &&
-                      fg::libgemm_ok(x_dtype, bias, bias_dtype, M, N, K, ldx, ldy, s) && workspace &&
+                      fg::libgemm_ok(x_dtype, x, bias, bias_dtype, y, M, N, K, ldx, ldy, s) && workspace &&
                       reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
                       workspace_bytes >= fg::libgemm_workspace_bytes((int)N, (int)K);
     if (fits)
@@ -695,9 +695,10 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
                         "fg_w8a16_gemm dequantise + library GEMM");
     if (impl == FG_W4_DEQUANT_GEMM)
       return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: the dequantise + library GEMM route needs K %% 16 == 0, group %% 16 "
-                                   "== 0 (or one group), ldq %% 16 == 0, 16-byte aligned qweight, a bias in fp32 or x's "
-                                   "dtype, a 256-byte aligned workspace of fg_w8a16_workspace_bytes and, under graph "
-                                   "capture, a first call of the same problem outside it");
+                                   "== 0 (or one group), ldq %% 16 == 0, 16-byte aligned qweight, x and y with 16-byte "
+                                   "aligned rows, a bias in fp32 or x's dtype, a 256-byte aligned workspace of "
+                                   "fg_w8a16_workspace_bytes and, under graph capture, a first call of the same "
+                                   "problem outside it");
   }
   const bool gemv = fg::w8a16_gemv_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);

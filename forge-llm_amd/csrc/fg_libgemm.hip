@@ -116,12 +116,14 @@ size_t libgemm_workspace_bytes(int N, int K) {
   return deq + kLtWorkspace;
 }
 
-// Whether the route applies to these operands: 16-bit x, a bias (if any) in fp32 or x's dtype, and a K hipBLASLt
-// reads with 16-byte rows.  Under graph capture only a problem whose handle and plan already exist takes it (creating
+// Whether the route applies to these operands: 16-bit x, a bias (if any) in fp32 or x's dtype, and x, y and K with
+// 16-byte aligned rows.  Under graph capture only a problem whose handle and plan already exist takes it (creating
 // them may allocate or synchronise, which a capture forbids); the caller's fused kernel serves the rest.
-bool libgemm_ok(int xdt, const void* bias, int bdt, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy,
-                   hipStream_t s) {
-  if (!((xdt == FG_BF16 || xdt == FG_F16) && (!bias || bdt == FG_F32 || bdt == xdt) && K % 8 == 0)) return false;
+bool libgemm_ok(int xdt, const void* x, const void* bias, int bdt, const void* y, int64_t M, int64_t N, int64_t K,
+                int64_t ldx, int64_t ldy, hipStream_t s) {
+  if (!((xdt == FG_BF16 || xdt == FG_F16) && (!bias || bdt == FG_F32 || bdt == xdt) && K % 8 == 0 && ldx % 8 == 0 &&
+        ldy % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0))
+    return false;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(s, &cs) != hipSuccess) return false;
   if (cs == hipStreamCaptureStatusNone) return true;

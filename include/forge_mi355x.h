@@ -41,7 +41,8 @@ enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_
    dequantised once into the workspace, then hipBLASLt's bf16 / fp16 GEMM (fp32 accumulation, bias in its epilogue);
    the policy takes it from 768 rows when the caller's workspace holds it
    (never in fg_w4a16_gemm_noalloc).  Needs
-   K % 8 == 0, no act-order perm (a g_idx is fine), a bias in fp32 or x's dtype, a 256-byte aligned workspace. */
+   K % 8 == 0, x and y with 16-byte aligned rows (ldx, ldy % 8 == 0), no act-order perm (a g_idx is fine), a bias
+   in fp32 or x's dtype, a 256-byte aligned workspace. */
 
 /* GEMV kernel selector (fg_w4_config.gemv_kernel) */
 enum { FG_GEMV_AUTO = 0, FG_GEMV_SPLIT = 1, FG_GEMV_TILE = 2, FG_GEMV_WAVE = 3 };
@@ -161,7 +162,8 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
  *            FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL
  *            (dequantise-to-LDS kernel), FG_W4_GENERIC (any shape), FG_W4_DEQUANT_GEMM (q * s rounded once to x's
  *            dtype into the workspace, then hipBLASLt's GEMM with the bias in its epilogue; needs K % 16 == 0,
- *            group % 16 == 0 or one group, ldq % 16 == 0, 16-byte aligned qweight, a bias in fp32 or x's dtype, a
+ *            group % 16 == 0 or one group, ldq % 16 == 0, 16-byte aligned qweight, x and y with 16-byte aligned rows,
+ *            a bias in fp32 or x's dtype, a
  *            256-byte aligned workspace and, under graph capture, a first call of the same problem outside it);
  *            split_k for the prefill kernel
  *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernel or, under the policy, of the

@@ -121,3 +121,17 @@ def test_graph_capture_uses_the_route_only_once_its_plan_exists():
         torch.cuda.synchronize()
         assert torch.equal(y2, routed), "captured call after the plan exists: not the route's bits"
         ops.w4a16_linear(x[:7], p)
+
+
+def test_unaligned_x_rows_stay_off_the_route():
+    """x rows K + 1 elements apart (2-byte aligned): the policy serves a 768-row call with another kernel (same bar);
+    forcing the route fails instead of handing hipBLASLt rows it does not take."""
+    m, n, k = 768, 512, 1024
+    q, s, z = w4_parts(n, k, 128, False, seed=61)
+    p = L.pack_w4(q, s, z, 128).to(DEV)
+    x = x_act(m, k + 1, torch.bfloat16, seed=62).to(DEV)[:, :k]
+    y = ops.w4a16_linear(x, p)
+    ref = og.w4a16_gemm_ref(to_f32(x.cpu()), oracle_packed(q, s, z, 128))
+    assert_close(y.cpu(), ref, "bfloat16", what="w4 unaligned x m=768")
+    with pytest.raises(ForgeError):
+        ops.w4a16_linear(x, p, config={"impl": "dequant_gemm"})

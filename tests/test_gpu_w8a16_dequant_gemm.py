@@ -117,3 +117,19 @@ def test_graph_capture_uses_the_route_only_once_its_plan_exists():
         torch.cuda.synchronize()
         assert torch.equal(y2, routed), "captured call after the plan exists: not the route's bits"
         ops.w8a16_linear(x[:7], p)
+
+
+def test_unaligned_x_rows_stay_off_the_route():
+    """x rows K + 1 elements apart (2-byte aligned): the policy serves a 768-row call with another kernel (same bar);
+    forcing the route fails instead of handing hipBLASLt rows it does not take."""
+    m, n, k = 768, 512, 1024
+    g = gen(51)
+    q = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, 1, generator=g) * 0.018 + 0.002).half()
+    p = L.pack_w8(q, s, -1).to(DEV)
+    x = x_act(m, k + 1, torch.bfloat16, 52).to(DEV)[:, :k]
+    y = ops.w8a16_linear(x, p)
+    ref = og.w8a16_gemm_ref(to_f32(x.cpu()), og.pack_w8(q.numpy(), s.float().numpy(), -1), None)
+    assert_close(y.cpu(), ref, "bfloat16", what="w8a16 unaligned x m=768")
+    with pytest.raises(ForgeError):
+        ops.w8a16_linear(x, p, config={"impl": "dequant_gemm"})
