@@ -32,7 +32,7 @@ hipError_t launch_w4_mfma(const void* x, int64_t ldx, bool xbf16, const int32_t*
 void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchunk, int* used);
 bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
                int64_t G);
-size_t w4_big_workspace_bytes(int M, int N, int K, int split_k);
+size_t w4_big_workspace_bytes(int M, int N, int K, int split_k, bool w8);
 bool w8a16_skinny_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int sdt, int64_t lds, int64_t M,
                      int64_t N, int64_t K, int gs, int64_t G);
 hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
@@ -358,7 +358,7 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
     // the launch picks among the skinny, prefill and tiled MFMA kernels once the operand addresses are known (an
     // act-order perm or misaligned operands rule some out): size the workspace for either split-K kernel
     if (prefill_ok) {
-      const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits);
+      const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits, false);
       if (wb > p->ws_bytes) p->ws_bytes = wb;
     }
     // ... and for the LDS-ring kernel when the policy sends the call there
@@ -655,7 +655,7 @@ size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return route;
   const size_t ring = impl == FG_W4_AUTO && w8a16_ring_rows(M, N, K) ? fg::w8a16_ring_workspace_bytes((int)M, (int)N, (int)K)
                                                                : 0;
-  return std::max({route, ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0)});
+  return std::max({route, ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0, true)});
 }
 
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
@@ -741,7 +741,7 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     e = fg::launch_w8a16_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
                                 (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (kern == 2) {
-    const size_t need = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0);
+    const size_t need = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0, true);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
       return fail(FG_EINVAL, "fg_w8a16_gemm: workspace of %zu bytes needed, %zu given", need,
                   workspace ? workspace_bytes : (size_t)0);

@@ -20,6 +20,8 @@
 //
 // Requirements (w4_big_ok): K % 64 == 0, group size a multiple of 32 (or one group), x 16-byte aligned with
 // ldx % 8 == 0, qweight 16-byte aligned with ldq % 4 == 0, no act-order perm.  Rows past M or N read row M-1 / N-1.
+#include <algorithm>
+
 #include "fg_device.h"
 
 namespace fg {
@@ -359,8 +361,9 @@ bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const
 
 // Row tile and K splits: 256 x 256 tiles when they alone cover the CUs, 64 x 256 for M <= 64, else 128 x 256, split
 // over K (in 64-column slices, at least 512 columns each) into as many parts as keep the workgroups within one round
-// over the CUs.
-void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kchunk) {
+// over the CUs.  8-bit weights over K >= 8192 take 256-row tiles from 129 rows when those fill the round at least as
+// well (each tile reads half as many weight bytes per row of x).
+void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kchunk, bool w8) {
   const int cus = device_cus();
   const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + kW4BigBN - 1) / kW4BigBN);
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + kW4BigBN - 1) / kW4BigBN);
@@ -369,16 +372,21 @@ void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kc
   // 132 us against 178 with 128-row tiles; gate+up M = 512, 224 tiles, 141 against 194; o_proj / down M = 2048 at 128
   // tiles stay on 128 rows: 98 / 319 us against 125 / 385)
   *bm = 4 * t256 >= 3 * cus ? 256 : (M <= 64 ? 64 : 128);
+  // as many splits as fit in one round of workgroups (gate+up at M = 64 / 128, 112 tiles: 2 splits take 57.5 / 71.3
+  // us, 3 -- a round and a third -- 60.1 / 85.0)
+  auto auto_splits = [&](int64_t tiles) {
+    int s = tiles >= cus ? 1 : (int)(cus / tiles);
+    const int max_s = K / 512 > 0 ? K / 512 : 1;
+    return s > max_s ? max_s : (s > 16 ? 16 : s);
+  };
+  // W8A16 down (K = 14336, N = 4096), us, 256- / 128-row tiles: M = 192 59.5 / 65.3, 384 93 / 96, 512 95 / 112, 640
+  // 130 / 137; K = 8192, N = 28672, M = 192 180 / 203 (4-bit weights and K = 4096 shapes: level or behind)
+  if (w8 && *bm == 128 && M > 128 && K >= 8192 && split_k <= 0 &&
+      std::min<int64_t>(t256 * auto_splits(t256), cus) >= std::min<int64_t>(t128 * auto_splits(t128), cus))
+    *bm = 256;
   const int64_t tiles = *bm == 256 ? t256 : (*bm == 128 ? t128 : t64);
   int s = split_k;
-  if (s <= 0) {
-    // as many splits as fit in one round of workgroups (gate+up at M = 64 / 128, 112 tiles: 2 splits take 57.5 / 71.3
-    // us, 3 -- a round and a third -- 60.1 / 85.0)
-    s = tiles >= cus ? 1 : (int)(cus / tiles);
-    const int max_s = K / 512 > 0 ? K / 512 : 1;
-    if (s > max_s) s = max_s;
-    if (s > 16) s = 16;
-  }
+  if (s <= 0) s = auto_splits(tiles);
   int kc = (K + s - 1) / s;
   const int unit = K % (2 * kW4BigBK) == 0 ? 2 * kW4BigBK : kW4BigBK;  // whole slice pairs where K allows them
   kc = (kc + unit - 1) / unit * unit;
@@ -386,9 +394,9 @@ void w4_big_plan(int M, int N, int K, int split_k, int* bm, int* splits, int* kc
   *splits = (K + kc - 1) / kc;
 }
 
-size_t w4_big_workspace_bytes(int M, int N, int K, int split_k) {
+size_t w4_big_workspace_bytes(int M, int N, int K, int split_k, bool w8) {
   int bm, s, kc;
-  w4_big_plan(M, N, K, split_k, &bm, &s, &kc);
+  w4_big_plan(M, N, K, split_k, &bm, &s, &kc, w8);
   return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
@@ -427,7 +435,7 @@ hipError_t launch_w4_big(const void* x, int64_t ldx, bool xbf16, const int32_t* 
                          int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
                          hipStream_t s) {
   int bm, splits, kchunk;
-  w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk);
+  w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk, false);
   const int gs32 = single_group ? 0 : gs / 32;
 #define FG_W4BIG(BM_, XB_)                                                                                             \
   return launch_w4_big_t<BM_, XB_, 4>(x, ldx, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy, ws, M, N, K, \
@@ -454,7 +462,7 @@ hipError_t launch_w8_big(const void* x, int64_t ldx, bool xbf16, const int8_t* q
                          int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M,
                          int N, int K, int gs, bool single_group, int split_k, hipStream_t s) {
   int bm, splits, kchunk;
-  w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk);
+  w4_big_plan(M, N, K, split_k, &bm, &splits, &kchunk, true);
   const int gs32 = single_group ? 0 : gs / 32;
 #define FG_W8BIG(BM_, XB_)                                                                                         \
   return launch_w4_big_t<BM_, XB_, 8>(x, ldx, qw, ldq, scales, sdt, lds, nullptr, 0, bias, bdt, y, ldy, ws, M, N, \

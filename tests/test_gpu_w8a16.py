@@ -116,7 +116,10 @@ def test_gemv_extremes_and_rejects():
         ops.w8a16_linear(x_act(1, 256, seed=84).to(DEV), L.pack_w8(q2, s2, -1).to(DEV), config={"impl": "gemv"})
 
 
-@pytest.mark.parametrize("m,n,k,gs", [(65, 256, 512, 32), (128, 777, 1024, -1), (300, 2048, 2048, 128)])
+# (200, 1024, 8192) and (390, 4096, 14336): 8-bit weights over K >= 8192 from 129 rows, where the plan takes 256-row
+# tiles (ragged last row tile, K split 16 / 5 ways)
+@pytest.mark.parametrize("m,n,k,gs", [(65, 256, 512, 32), (128, 777, 1024, -1), (300, 2048, 2048, 128),
+                                      (200, 1024, 8192, 128), (390, 4096, 14336, -1)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_prefill_matches_oracle(m, n, k, gs, xdt):
     y, ref = _case(m, n, k, gs, xdt, seed=m + k, config={"impl": "prefill"})
