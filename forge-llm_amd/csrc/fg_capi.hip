@@ -199,10 +199,13 @@ int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t l
   }
   if (big_ok) {
     // Measured on the configs' shapes (us, bf16 output, random operands):
-    //  * the skinny kernel only for M <= 16 at K >= 16384 (int8 K=28672, N=8192: 45 / 56 at M = 1 / 16 against 58 /
-    //    60 for the ring kernel); at K = 8192 the ring kernel is ahead from M = 1 (int8 N=10240: 20 against 27; fp8
-    //    N=8192 at M=16: 17 against 19; int8 N=57344: 96 against 112), and at M = 32..64 everywhere (int8 K=28672,
-    //    M=64: 63 against 139);
+    //  * the skinny kernel for M <= 16 at K >= 16384 (int8 K=28672, N=8192: 45 / 56 at M = 1 / 16 against 58 / 60 for
+    //    the ring kernel), and for M <= 32 where the ring's 64 x 32 tiles would not cover the CUs (int8 K=14336,
+    //    N=4096: 15.3 / 22.6 / 26.0 at M = 4 / 24 / 32 against 29.6-30.1; fp8 K=N=4096: 6.8 / 9.0 against 9.6 / 9.8 at
+    //    M = 4 / 24, level at 32, behind from 48); with the CUs covered the ring kernel is ahead from M = 1 (int8 K=8192,
+    //    N=10240: 20 against 27; fp8 N=8192 at M=16: 17 against 19; int8 N=57344: 96 against 112; K=4096, N=14336 or
+    //    28672: 15.8 / 27.8 against 19.1 / 32.7 at M = 4), and at M = 32..64 everywhere (int8 K=28672, M=64: 63
+    //    against 139);
     //  * the 256-row kernel once its tiles number 5/8 of the CUs, whatever M (int8 M=1024, K=8192, N=10240: 160 tiles,
     //    113 against 130 for 128-row ring tiles; K=8192, M=160..224, N=57344: 224 tiles, 146-150 against 180-186
     //    int8 and 150-156 against 168-180 fp8; M=300..448, N=28672: 118-128 against 131-177; M=640, N=14336: 168
@@ -212,8 +215,8 @@ int mm_tile(int64_t M, int64_t N, int64_t K, bool int8, const void* a, int64_t l
     //    62 for 64 x 128) unless 64 x 128 tiles fit one per CU (int8 K=8192, N=10240, M=160..192: 240 tiles, 34-35
     //    against 41; M=224: 320 tiles, 57 against 43), else 64-row tiles (fp8 M=256: 33 against 65 for the
     //    register-staged 64 x 64 tiles).
-    if (skinny_ok && M <= 16 && K >= 16384) return 16;
     const int64_t tiles = fg::mm_big_tiles(M, N), cus = fg::device_cus();
+    if (skinny_ok && ((M <= 16 && K >= 16384) || (M <= 32 && (N + 31) / 32 < cus))) return 16;
     if (8 * tiles >= 5 * cus) return 256;
     *ring = true;
     const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128), t64 = ((M + 63) / 64) * ((N + 127) / 128);

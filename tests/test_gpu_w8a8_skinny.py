@@ -1,7 +1,8 @@
 """GPU parity of the skinny W8A8 kernel (fg_w8_skinny.hip, M <= 64, register-resident split-K): INT8 accumulator and
 fp32 / bf16 / fp16 epilogues bit-exact against the CPU oracle (the int32 partials of the K slices sum exactly), FP8
 within the north-star bar, as is the 64-row kernel on the same inputs; forced with tile_m=16, and the policy's own choice
-(the skinny kernel for M <= 16 at K >= 16384, the ring kernel for the other aligned shapes) held to the same bar."""
+(the skinny kernel for M <= 16 at K >= 16384 and for M <= 32 where the ring's 64 x 32 tiles would not cover the CUs,
+the ring kernel for the other aligned shapes) held to the same bar."""
 from __future__ import annotations
 
 import numpy as np
@@ -80,3 +81,26 @@ def test_skinny_reproducible_and_rejects():
     with pytest.raises(_lib.KernelLaunchError, match="tile_m=16"):
         ops.int8_gemm(a2, None, w2, None, out_dtype=torch.int32, config=SK)  # K % 256 != 0
     assert ops.int8_gemm(a2, None, w2, None, out_dtype=torch.int32).abs().sum().item() == 0  # policy falls back
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 4096, 14336), (24, 4096, 14336), (8, 4096, 4096), (32, 2048, 4096)])
+def test_policy_skinny_for_narrow_outputs(m, n, k):
+    """M <= 32 over N < 32 x CUs (fewer 64 x 32 ring tiles than CUs): the policy's INT8 and FP8 results equal the forced
+    skinny kernel's bit for bit and match the oracle (INT8 bf16 output exactly)."""
+    xq, sx, wq, sw = _i8(m, n, k, seed=m + n + k)
+    a, w = torch.from_numpy(xq).to(DEV), torch.from_numpy(wq).to(DEV)
+    ta, tb = torch.from_numpy(sx).to(DEV), torch.from_numpy(sw).to(DEV)
+    y = ops.int8_gemm(a, ta, w, tb, out_dtype=torch.bfloat16)
+    assert torch.equal(y, ops.int8_gemm(a, ta, w, tb, out_dtype=torch.bfloat16, config=SK))
+    ref = og.int8_gemm_ref(xq, sx, wq, sw, None, acc=og.int8_matmul_exact(xq, wq))
+    assert torch.equal(y.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+    x = torch.randn(m, k, generator=gen(m + 7)).to(torch.bfloat16)
+    wf = torch.randn(n, k, generator=gen(n + 8)) * 0.05
+    fq, fsx = og.quantize_fp8_ref(to_f32(x), "per_token")
+    gq, gsw = og.quantize_fp8_ref(wf.numpy(), "per_channel")
+    txq = torch.from_numpy(fq).view(torch.float8_e4m3fn).to(DEV)
+    twq = torch.from_numpy(gq).view(torch.float8_e4m3fn).to(DEV)
+    tsx, tsw = torch.from_numpy(fsx).to(DEV), torch.from_numpy(gsw).to(DEV)
+    yf = ops.fp8_linear(txq, twq, tsw, x_scale=tsx, out_dtype=torch.bfloat16)
+    assert torch.equal(yf, ops.fp8_linear(txq, twq, tsw, x_scale=tsx, out_dtype=torch.bfloat16, config=SK))
+    assert_close(yf.cpu(), og.fp8_gemm_ref(fq, fsx, gq, gsw), "bfloat16", what=f"fp8 policy skinny m={m} n={n} k={k}")
