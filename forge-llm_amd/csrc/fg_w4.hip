@@ -716,8 +716,8 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 }
 
 // Launch shape of the split-K GEMV: S chunks per lane (1 while K <= 32768, else 2 for one row of x), KS =
-// ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront (8 for wide outputs or long K, else 4; R * MT <=
-// 16), BW channel blocks per workgroup (8 .. 16 wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
+// ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront (16 for one row of x over 8 or more slices, 8 for
+// wide outputs or long K, else 4; R * MT <= 16), BW channel blocks per workgroup (8 .. 16 wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
 bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) {
   const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
   const int s = KC <= 16 * kWave ? 1 : (KC <= 32 * kWave && mt == 1 ? 2 : 0);
@@ -728,6 +728,9 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
   // 448 workgroups of 16 wavefronts against 13.2 with 16 rows in one workgroup per CU; qkv 4.75 against 5.03 with 8
   // rows): fewer rows per wavefront shorten the arithmetic left once a wavefront's last bytes arrive
   int r = (per_cu >= 64 || ks >= 4) ? 8 : 4;
+  // one row of x split 8 or more ways over K: 16 rows per wavefront, half the wavefronts (K = 28672, N = 8192: 26.3 us
+  // against 32.3 with 8 rows; K = 14336, 7 slices: level)
+  if (mt == 1 && ks >= 8) r = 16;
   if (mt == 2) r = min(r, 8);
   if (mt == 4) r = 4;
   if (s == 2) r = 4;  // 8 rows x 2 chunks would spill

@@ -76,12 +76,18 @@ def test_gemv_kernels_match_oracle(kernel, case):
 
 
 @pytest.mark.parametrize("m,n,k,gs,sdt", [(1, 256, 40000, 128, torch.float16), (1, 64, 65536, 64, torch.float32),
-                                          (4, 96, 16384, 32, torch.bfloat16), (2, 64, 32768, 128, torch.float16)])
+                                          (4, 96, 16384, 32, torch.bfloat16), (2, 64, 32768, 128, torch.float16),
+                                          (1, 1024, 28672, 128, torch.float16), (1, 200, 16384, 64, torch.bfloat16)])
 def test_split_gemv_long_k(m, n, k, gs, sdt):
-    """Two 16-byte chunks per lane and 10-16 K slices (K > 32768), and the K limits of 2 and 4 rows of x."""
+    """Two 16-byte chunks per lane and 10-16 K slices (K > 32768); 16 channels per wavefront over 8-14 slices for one
+    row of x (K = 16384..28672; N = 200 takes the bounds-checked form); the K limits of 2 and 4 rows of x.  Forced and
+    through the policy."""
     cfg = {"impl": "gemv", "gemv_kernel": "split"}
     y, ref = _case(m, n, k, gs, m == 4, torch.bfloat16, bias=m == 1, seed=k, scale_dtype=sdt, config=cfg)
     assert_close(y.cpu(), ref, "bfloat16", what=f"split m={m} n={n} k={k}")
+    if m == 1:
+        y2, _ = _case(m, n, k, gs, False, torch.bfloat16, bias=True, seed=k, scale_dtype=sdt)
+        assert_close(y2.cpu(), ref, "bfloat16", what=f"policy m={m} n={n} k={k}")
 
 
 def test_split_gemv_limits_and_unaligned_x():
