@@ -741,7 +741,9 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
   // blocks of 8 rows: 448 workgroups of 16 wavefronts 12.2 us against 12.6 for 896 of 8 and 14.4 for 1195 of 12) and
   // 8-16 wavefronts otherwise.
   const int nblk = (N + r - 1) / r, cus = device_cus();
-  int bw = nblk >= 8 * cus ? max_waves / ks : max(2, 8 / ks);
+  // two rows of x over wide outputs: two channel blocks per workgroup (4-8 wavefronts; M = 2, us, gate+up 15.8 against
+  // 18.6 with the widest workgroups, K = 8192, N = 57344 56.0 against 62.5)
+  int bw = nblk >= 8 * cus ? (mt == 2 ? 2 : max_waves / ks) : max(2, 8 / ks);
   if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) bw = nblk / cus;
   while (bw * ks > max_waves && bw > 1) --bw;
   *S = s; *R = r; *KS = ks; *BW = bw;
