@@ -446,7 +446,10 @@ struct W8GemvPlan {
 static bool w8a16_gemv_plan(int M, int N, int K, W8GemvPlan* p) {
   const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
   const int KC = K / 16, R = mt == 4 ? 4 : 8;
-  const int S = KC <= 4 * kWave ? 1 : (mt == 4 ? 2 : 4);
+  // one chunk per lane while the K slices fit one workgroup (1-2 rows: K <= 16384), else 4 (2 for four rows).  Graph
+  // replays, us, one chunk / four: K = 8192, N = 10240 / 8192 / 57344 15.6 / 12.9 / 74.8 against 18.9 / 16.2 / 83.9;
+  // K = 14336, N = 4096 12.0 / 12.5 (M = 1 / 2) against 12.4 / 14.3; K = 28672 (28 slices) stays on four
+  const int S = KC <= 4 * kWave || (mt <= 2 && KC <= 16 * kWave) ? 1 : (mt == 4 ? 2 : 4);
   const int ks = (KC + kWave * S - 1) / (kWave * S);
   const int maxw = w8a16_gemv_max_threads(mt) / kWave;
   if (ks > maxw || N % R != 0) return false;

@@ -73,7 +73,7 @@ def test_ring_reproducible_and_level_with_skinny():
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("n,k,gs", [(4096, 4096, -1), (776, 2048, 128), (1032, 1024, 256), (512, 960, 48),
-                                    (264, 20480, 128), (8, 16, 16)])
+                                    (264, 20480, 128), (8, 16, 16), (1024, 8192, 128), (520, 14336, -1)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_gemv_matches_oracle(m, n, k, gs, xdt):
     """The split-K decode GEMV forced (one, two and four chunks per lane, group sizes that are not powers of two, a K
