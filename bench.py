@@ -140,7 +140,8 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
 
             t = timer(torch, run, steps, warmup) / len(sel)
             gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
-            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "kernel": ops.last_kernel()}
         decode[f"M{m}"] = row
         log(f"decode M={m}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
     # the same weights repacked at load time into the CDNA4 MFMA-fragment layout (a bit-exact permutation), read by
@@ -161,7 +162,8 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
 
             t = timer(torch, run, steps, warmup) / len(sel)
             gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
-            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "kernel": ops.last_kernel()}
         decode[f"M{m}_cdna4_layout"] = row
         log(f"decode M={m} (cdna4 layout): " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s"
                                                        for nm, v in row.items()))
@@ -179,13 +181,15 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
                     ops.w4a16_linear(x, p)
 
             t = time_graph(torch, run, max(5, steps // 2), 2)
+            kern = ops.last_kernel()
             ms = t / len(ws)
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
             # the reference's large-M route after its dequantised copy: hipBLASLt's bf16 GEMM via F.linear
             vend = time_graph(torch, lambda x=x, w=dense[name]: torch.nn.functional.linear(x, w),
                               max(5, steps // 2), 2)
             row[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                         "median_ms": round(t.median / len(ws), 4), "vendor_bf16_gemm_ms": round(vend, 4)}
+                         "median_ms": round(t.median / len(ws), 4), "kernel": kern,
+                         "vendor_bf16_gemm_ms": round(vend, 4)}
             del x
         prefill[f"M{m}"] = row
         log(f"prefill M={m}: " + "  ".join(f"{nm} {v['ms']:.3f} ms {v['tflops']:.0f} TF" for nm, v in row.items()))
@@ -214,7 +218,7 @@ def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -
             t = timer(torch, run, steps, warmup) / len(ring)
             by = n * k + 2 * n + 2 * m * (k + n)
             row[f"M{m}"] = {"us": round(t * 1e3, 3), "GBps": round(by / (t * 1e-3) / 1e9, 1),
-                            "frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                            "frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": ops.last_kernel()}
         out[name] = row
         log(f"w8a16 {name:8s}: " + "  ".join(f"M={mm[1:]} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for mm, v in row.items()))
         del ring
@@ -247,7 +251,8 @@ def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
         by = n * k + m * k + 4 * (m + n) + 2 * m * n
         out[f"fp8_m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
                                       "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1),
-                                      "median_us": round(t.median / len(ring) * 1e3, 2)}
+                                      "median_us": round(t.median / len(ring) * 1e3, 2),
+                                      "kernel": ops.last_kernel()}
         log(f"fp8 M={m} K=N=8192: {ms * 1e3:.1f} us  {out[f'fp8_m{m}_k{k}_n{n}']['GBps']:.0f} GB/s")
     del ring
     for (k8, n8) in ((8192, 10240), (8192, 57344), (28672, 8192)):
@@ -268,7 +273,7 @@ def bench_w8a8_small(torch, ops, dev, reps: int) -> dict:
             key = f"int8_m{m}_k{k8}_n{n8}"
             out[key] = {"us": round(ms * 1e3, 2), "GBps": round(by / (ms * 1e-3) / 1e9, 1),
                         "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                        "median_us": round(t.median / len(ring) * 1e3, 2)}
+                        "median_us": round(t.median / len(ring) * 1e3, 2), "kernel": ops.last_kernel()}
             log(f"int8 M={m} K={k8} N={n8}: {ms * 1e3:.1f} us  {out[key]['GBps']:.0f} GB/s")
         del ring
     return out
@@ -300,7 +305,8 @@ def bench_w8a8(torch, ops, dev, reps: int) -> dict:
     flops = 2.0 * m * n * k
     t = time_eager(torch, lambda: ops.fp8_linear(xq, wq, sw, x_scale=sx, out_dtype=torch.bfloat16), reps, 3)
     tf = flops / (t * 1e-3) / 1e12
-    row = {"ms": round(t, 4), "tflops": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4), **t.stats()}
+    row = {"ms": round(t, 4), "tflops": round(tf, 1), "frac": round(tf / FP8_PEAK_TFLOPS, 4), **t.stats(),
+           "kernel": ops.last_kernel()}
     wt = wq.t()
     vend = _vendor(torch, lambda: torch._scaled_mm(xq, wt, scale_a=sx.reshape(m, 1), scale_b=sw.reshape(1, n),
                                                    out_dtype=torch.bfloat16), reps)
@@ -319,7 +325,8 @@ def bench_w8a8(torch, ops, dev, reps: int) -> dict:
         t = time_eager(torch, lambda: ops.int8_linear(xi, wi, swi, x_scale=sxi, out_dtype=torch.bfloat16), reps, 3)
         ops_n = 2.0 * m * n8 * k8
         tops = ops_n / (t * 1e-3) / 1e12
-        row = {"ms": round(t, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), **t.stats()}
+        row = {"ms": round(t, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4), **t.stats(),
+               "kernel": ops.last_kernel()}
         wti = wi.t()
         vend = _vendor(torch, lambda: torch._int_mm(xi, wti), reps)
         if vend is not None:
@@ -543,7 +550,7 @@ def main() -> None:
         gbs = w4_bytes(1, k, n) / (t * 1e-3) / 1e9
         per_shape[name] = {"K": k, "N": n, "us": round(t * 1e3, 3), "GBps": round(gbs, 1),
                            "frac": round(gbs / HBM_PEAK_GBS, 4), "median_us": round(tt.median / len(sel) * 1e3, 3),
-                           "iqr_us": round(tt.iqr / len(sel) * 1e3, 3)}
+                           "iqr_us": round(tt.iqr / len(sel) * 1e3, 3), "kernel": ops.last_kernel()}
         log(f"  {name:8s} K={k:5d} N={n:5d}: {t * 1e3:8.3f} us  {gbs:7.1f} GB/s")
     copy_bw = measure_copy_bandwidth(torch, dev)
     log(f"copy bandwidth: {copy_bw['GBps']:.0f} GB/s")

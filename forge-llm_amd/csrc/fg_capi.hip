@@ -152,6 +152,21 @@ hipError_t launch_quant_fp8_block(const void* x, int64_t ldx, int xdt, uint8_t* 
                                   hipStream_t st);
 }  // namespace fg
 
+namespace fg {
+
+namespace {
+thread_local char g_kernel[160];
+}
+
+void note_kernel(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_kernel, sizeof(g_kernel), fmt, ap);
+  va_end(ap);
+}
+
+}  // namespace fg
+
 namespace {
 
 thread_local std::string g_err;
@@ -236,6 +251,8 @@ extern "C" {
 const char* fg_version(void) { return "forge_mi355x 0.1.0 (gfx950)"; }
 
 const char* fg_last_error(void) { return g_err.c_str(); }
+
+const char* fg_last_kernel(void) { return fg::g_kernel; }
 
 int fg_device_ok(int device) {
   hipDeviceProp_t prop;

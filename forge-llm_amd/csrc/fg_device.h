@@ -14,6 +14,10 @@ namespace fg {
 
 constexpr int kWave = 64;
 
+// Records (printf-style) the kernel and launch form of the calling thread's current launch; fg_last_kernel() returns
+// it.  Host code only.
+void note_kernel(const char* fmt, ...);
+
 // ----------------------------------------------------------------------------------------------- conversions
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

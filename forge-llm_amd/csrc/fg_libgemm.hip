@@ -195,13 +195,15 @@ hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t*
                              const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
                              void* ws, size_t ws_bytes, hipStream_t s) {
   const size_t esz = sdt == FG_F32 ? 4 : 2;
-  return libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
+  const hipError_t e = libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
                      [&](int n0, int nc, void* out, hipStream_t st) {
                        return launch_w4_dequant(qw + (int64_t)n0 * ldq, ldq,
                                                 static_cast<const uint8_t*>(scales) + (size_t)n0 * esz, sdt, lds,
                                                 zeros ? zeros + n0 / 8 : nullptr, ldz, g_idx, out, xdt, K, nc, K, gs,
                                                 st);
                      });
+  note_kernel("w4_dequant16_kernel + hipBLASLt GEMM");
+  return e;
 }
 
 // W8A16: symmetric int8 weights [N, ldq] with scales [G, lds] (w8_dequant16_ok must hold).
@@ -209,12 +211,14 @@ hipError_t launch_w8a16_libgemm(const void* x, int64_t ldx, int xdt, const int8_
                                 int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
                                 int K, int gs, void* ws, size_t ws_bytes, hipStream_t s) {
   const size_t esz = sdt == FG_F32 ? 4 : 2;
-  return libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
+  const hipError_t e = libgemm_run(x, ldx, xdt, bias, bdt, y, ldy, M, N, K, ws, ws_bytes, s,
                      [&](int n0, int nc, void* out, hipStream_t st) {
                        return launch_w8_dequant16(qw + (int64_t)n0 * ldq, ldq,
                                                   static_cast<const uint8_t*>(scales) + (size_t)n0 * esz, sdt, lds, out,
                                                   xdt, K, nc, K, gs, st);
                      });
+  note_kernel("w8_dequant16_kernel + hipBLASLt GEMM");
+  return e;
 }
 
 }  // namespace fg

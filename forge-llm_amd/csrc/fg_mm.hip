@@ -168,6 +168,7 @@ static hipError_t launch_mm(const uint8_t* A, int64_t lda, const uint8_t* B, int
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     if (e != hipSuccess) return e;
   }
+  note_kernel("mm_kernel %dx%d", BM, BN);
   hipLaunchKernelGGL(k, dim3(tiles), dim3(256), shm, s, A, lda, B, ldb, M, N, K, epi);
   return hipGetLastError();
 }

@@ -354,6 +354,7 @@ static hipError_t launch_big_t(const uint8_t* A, int64_t lda, const uint8_t* B, 
                                      (int)lds);
   if (e != hipSuccess) return e;
   const unsigned tiles = (unsigned)(((M + kBigBM - 1) / kBigBM) * ((N + BN - 1) / BN));
+  note_kernel("mm_big_kernel 256x%d", BN);
   hipLaunchKernelGGL(k, dim3(tiles), dim3(kBigWM * kBigWN * 64), lds, s, A, lda, B, ldb, M, N, K, epi);
   return hipGetLastError();
 }
@@ -417,6 +418,7 @@ static hipError_t launch_ring_t(const uint8_t* A, int64_t lda, const uint8_t* B,
                                      (int)lds);
   if (e != hipSuccess) return e;
   const unsigned tiles = (unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+  note_kernel("mm_ring_kernel %dx%d S=%d", BM, BN, S);
   hipLaunchKernelGGL(k, dim3(tiles), dim3(WM * WN * 64), lds, s, A, lda, B, ldb, M, N, K, epi);
   return hipGetLastError();
 }

@@ -115,8 +115,11 @@ hipError_t launch_int8_gemv(const int8_t* a, int64_t lda, const float* sa, int64
   g.bbytes = (uint32_t)((int64_t)N * ldb);
   const EpiInt8 epi{sa, sa_len, sb, sb_len, bias, bdt, y, ldy, ydt};
   const dim3 grid(N / 8), block(kWave, KS);
-#define FG_I8G(MT_, S_) \
-  hipLaunchKernelGGL((int8_gemv_kernel<MT_, S_>), grid, block, 0, s, a, lda, b, ldb, M, N, g, epi)
+#define FG_I8G(MT_, S_)                                                                              \
+  do {                                                                                               \
+    note_kernel("int8_gemv_kernel<%d,%d>", MT_, S_);                                                 \
+    hipLaunchKernelGGL((int8_gemv_kernel<MT_, S_>), grid, block, 0, s, a, lda, b, ldb, M, N, g, epi); \
+  } while (0)
   if (mt == 1) {
     if (S == 1) FG_I8G(1, 1); else if (S == 2) FG_I8G(1, 2); else FG_I8G(1, 4);
   } else {

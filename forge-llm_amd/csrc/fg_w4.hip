@@ -775,6 +775,7 @@ static hipError_t launch_split_t(bool fast, const void* x, int64_t ldx, const in
   auto kern = !fast ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitGeneral>
                     : (sdt == FG_BF16 ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales>
                                       : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales>);
+  note_kernel("w4_gemv_split_kernel<%d,%d,%d,%s>%s KS=%d", MT, S, R, XBF16 ? "bf16" : "f16", fast ? "" : " general", KS);
   hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const uint16_t*>(x), ldx, perm, qw, ldq, scales, sdt, lds, zp,
                      ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, a);
   return hipGetLastError();
@@ -980,6 +981,7 @@ static hipError_t launch_gemv_t(const void* x, int64_t ldx, const int32_t* qw, i
   const int NB = (N + R - 1) / R;
   int blocks = (NB + waves - 1) / waves;
   if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
+  note_kernel("w4_gemv_kernel<%d,%d,%s>", MT, R, XBF16 ? "bf16" : "f16");
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(threads), shm, stream, static_cast<const uint16_t*>(x), ldx, qw, ldq,
                      scales, sdt, lds, zeros, ldz, perm, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gs);
   return hipGetLastError();
@@ -1027,6 +1029,7 @@ static hipError_t launch_gemv_tile_t(const void* x, int64_t ldx, const int32_t* 
     if (e != hipSuccess) return e;
   }
   const int blocks = (N + tp.tn - 1) / tp.tn;
+  note_kernel("w4_gemv_tile_kernel<%d,%d,%s> TN=%d", MT, S, XBF16 ? "bf16" : "f16", tp.tn);
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(tp.waves * kWave), tp.lds, s, static_cast<const uint16_t*>(x), ldx, qw,
                      ldq, scales, sdt, lds, zeros, ldz, perm, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gs, G,
                      tp.tn, tp.waves);
@@ -1108,6 +1111,7 @@ hipError_t launch_w4_generic(const void* x, int64_t ldx, int xdt, const int32_t*
                              int K, int gs, hipStream_t s) {
   const int64_t nwork = (int64_t)N * ((M + 3) / 4);
   const int64_t blocks = (nwork + 3) / 4;
+  note_kernel("w4_generic_kernel");
   hipLaunchKernelGGL(w4_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const uint16_t*>(x), ldx,
                      xdt, qw, ldq, scales, sdt, lds, zeros, ldz, perm, g_idx, bias, bdt, static_cast<uint16_t*>(y),
                      ldy, M, N, K, gs);
@@ -1127,12 +1131,14 @@ hipError_t launch_w4_dequant(const int32_t* qw, int64_t ldq, const void* scales,
     const uint32_t gdiv = one_group ? 0u : (uint32_t)gs;
     const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;  // c / gs = umulhi(c, gmul)
     auto kern = odt == FG_BF16 ? w4_dequant16_kernel<true> : w4_dequant16_kernel<false>;
+    note_kernel("w4_dequant16_kernel");
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, static_cast<const uint16_t*>(scales),
                        (int)(sdt == FG_BF16), lds, zeros, ldz, static_cast<uint16_t*>(out), ldo, N, K, wpr, gdiv, gmul);
     return hipGetLastError();
   }
   const int64_t total = (int64_t)N * ((K + 7) / 8);
   const int64_t blocks = (total + 255) / 256;
+  note_kernel("w4_dequant_kernel");
   hipLaunchKernelGGL(w4_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, scales, sdt, lds, zeros, ldz,
                      g_idx, out, odt, ldo, N, K, gs);
   return hipGetLastError();

@@ -422,6 +422,8 @@ static hipError_t launch_w4_big_t(const void* x, int64_t ldx, const void* qw, in
   const int32_t* zp = hasz ? zeros : static_cast<const int32_t*>(qw);  // symmetric: a valid dummy word, ignored
   const int64_t ldzp = hasz ? ldz : 0;
   const int tiles = ((M + BM - 1) / BM) * ((N + kW4BigBN - 1) / kW4BigBN);
+  note_kernel("w4_big_kernel<%d,%s,w%d> splits=%d%s", BM, XBF16 ? "bf16" : "f16", WB, splits,
+              splits > 1 ? " + w4_splitk_reduce_kernel" : "");
   hipLaunchKernelGGL(kern, dim3(tiles, splits), dim3(kW4BigThreads), shm, s, static_cast<const uint16_t*>(x), ldx, qw,
                      ldq, scales, sdt, lds, zp, ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, ws, M, N, K,
                      gs32, kchunk);

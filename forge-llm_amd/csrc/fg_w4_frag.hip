@@ -247,6 +247,7 @@ static hipError_t launch_frag_t(const void* x, int64_t ldx, const int32_t* qw, i
   const int64_t nt = (N + 15) / 16;
   const FragSpans sp{(uint32_t)(nt * ldq * 4), (uint32_t)((int64_t)M * ldx * 2), (uint32_t)((int64_t)G * lds * 2),
                      hasz ? (uint32_t)((int64_t)G * ldz * 4) : 4u};
+  note_kernel("w4_frag_kernel KS=%d", KS);
   hipLaunchKernelGGL(kern, dim3(nblk), dim3(kWave * KS), shm, s, static_cast<const uint16_t*>(x), ldx, qw, ldq,
                      static_cast<const uint16_t*>(scales), lds, zp, hasz ? ldz : 0, hasz, bias, bdt,
                      static_cast<uint16_t*>(y), ldy, M, N, K, gsteps, KS, sp);

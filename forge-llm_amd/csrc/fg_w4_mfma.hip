@@ -270,6 +270,7 @@ static hipError_t launch_w4_mfma_t(const void* x, int64_t ldx, const int32_t* qw
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   int kchunk = 0, used = 0;
   w4_mfma_split_plan(M, N, K, BM, splits, &kchunk, &used);
+  note_kernel("w4_mfma_kernel splits=%d%s", used, used > 1 ? " + w4_splitk_reduce_kernel" : "");
   hipLaunchKernelGGL(kern, dim3(tiles, used), dim3(256), shm, s, static_cast<const uint16_t*>(x), ldx, perm, qw, ldq,
                      scales, sdt, lds, zeros, ldz, bias, bdt, static_cast<uint16_t*>(y), ldy, ws, M, N, K, gs, kchunk);
   hipError_t e = hipGetLastError();

@@ -526,6 +526,8 @@ static hipError_t launch_ring_t(const RingArgs& a, hipStream_t s) {
   using Sh = RingShape<MB, T, BW>;
   const size_t shm = (size_t)S * Sh::STAGE + Sh::XS;
   auto kern = w4_ring_kernel<MB, T, BW, S, XBF16, SBF16, PORT>;
+  note_kernel("w4_ring_kernel<%d,%d,%d,%d,%s,%s> KS=%d%s", MB, T, BW, S, XBF16 ? "bf16" : "f16",
+              PORT ? "portable_row" : "cdna4", a.KS, a.KS > 1 ? " + w4_ring_reduce_kernel" : "");
   if (shm > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -613,6 +615,8 @@ static hipError_t launch_w8ring_t(const RingArgs& a, hipStream_t s) {
   using Sh = RingShape<MB, T, BW, true>;
   const size_t shm = (size_t)S * Sh::STAGE + Sh::XS;
   auto kern = w8a16_ring_kernel<MB, T, BW, S, XBF16, SBF16>;
+  note_kernel("w8a16_ring_kernel<%d,%d,%d,%d,%s> KS=%d%s", MB, T, BW, S, XBF16 ? "bf16" : "f16", a.KS,
+              a.KS > 1 ? " + w4_ring_reduce_kernel" : "");
   if (shm > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);

@@ -254,6 +254,7 @@ static hipError_t launch_skinny_t(const void* x, int64_t ldx, const int32_t* qw,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     if (e != hipSuccess) return e;
   }
+  note_kernel("w4_skinny_kernel KS=%d", KS);
   hipLaunchKernelGGL(kern, dim3((nblk + BW - 1) / BW), dim3(kWave * BW * KS), shm, s,
                      static_cast<const uint16_t*>(x), ldx, qw, ldq, static_cast<const uint16_t*>(scales), lds, zp,
                      hasz ? ldz : 0, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gsteps, KS);

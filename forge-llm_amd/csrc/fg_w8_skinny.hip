@@ -172,6 +172,7 @@ static hipError_t launch_w8sk_t(const uint8_t* a, int64_t lda, const uint8_t* b,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     if (e != hipSuccess) return e;
   }
+  note_kernel("w8_skinny_kernel KS=%d", KS);
   hipLaunchKernelGGL(kern, dim3((nblk + BW - 1) / BW), dim3(kWave * BW * KS), shm, s, a, lda, b, ldb, M, N, K, KS,
                      epi);
   return hipGetLastError();

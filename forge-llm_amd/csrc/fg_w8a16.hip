@@ -394,6 +394,7 @@ static hipError_t launch_w8a16_skinny_t(const void* x, int64_t ldx, const int8_t
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
     if (e != hipSuccess) return e;
   }
+  note_kernel("w8a16_skinny_kernel KS=%d", KS);
   hipLaunchKernelGGL(kern, dim3((nblk + BW - 1) / BW), dim3(kWave * BW * KS), shm, s,
                      static_cast<const uint16_t*>(x), ldx, qw, ldq, static_cast<const uint16_t*>(scales), lds, bias,
                      bdt, static_cast<uint16_t*>(y), ldy, M, N, K, gsteps, KS);
@@ -481,6 +482,7 @@ static hipError_t launch_w8a16_gemv_t(const W8GemvPlan& p, const void* x, int64_
   a.xbytes = (uint32_t)((int64_t)M * ldx * 2);
   a.sbytes = (uint32_t)(G * lds * 2);
   const int nblk = N / R;
+  note_kernel("w8a16_gemv_kernel<%d,%d,%d>", MT, S, R);
   hipLaunchKernelGGL((w8a16_gemv_kernel<MT, S, R, XBF16, SBF16>), dim3((nblk + p.BW - 1) / p.BW),
                      dim3(kWave * p.BW, p.KS), 0, s, static_cast<const uint16_t*>(x), ldx, qw, ldq,
                      static_cast<const uint16_t*>(scales), lds, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, a);
@@ -526,6 +528,7 @@ hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_
                                 const void* scales, int sdt, int64_t lds, const void* bias, int bdt, void* y,
                                 int64_t ldy, int M, int N, int K, int gs, hipStream_t s) {
   const int64_t waves = (int64_t)N * ((M + 3) / 4);
+  note_kernel("w8a16_generic_kernel");
   hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, ldx, xdt, qw, ldq,
                      scales, sdt, lds, bias, bdt, y, ldy, M, N, K, gs);
   return hipGetLastError();
@@ -601,6 +604,7 @@ hipError_t launch_w8_dequant16(const int8_t* qw, int64_t ldq, const void* scales
   const uint32_t gdiv = G == 1 ? 0u : (uint32_t)gs;
   const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;
   auto kern = odt == FG_BF16 ? w8_dequant16_kernel<true> : w8_dequant16_kernel<false>;
+  note_kernel("w8_dequant16_kernel");
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, scales, sdt, lds,
                      static_cast<uint16_t*>(out), ldo, N, K, wpr, gdiv, gmul);
   return hipGetLastError();

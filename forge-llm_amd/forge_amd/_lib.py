@@ -79,6 +79,7 @@ SIGNATURES = {
     "fg_quant_fp8_block": ([P, I64, INT, P, I64, P, I64, I64, I64, I32_, I32_, P, P], INT),
     "fg_version": ([], ctypes.c_char_p),
     "fg_last_error": ([], ctypes.c_char_p),
+    "fg_last_kernel": ([], ctypes.c_char_p),
     "fg_device_ok": ([INT], INT),
 }
 
@@ -110,6 +111,11 @@ def lib():
 
 def last_error() -> str:
     return (lib().fg_last_error() or b"").decode()
+
+
+def last_kernel() -> str:
+    """The kernel (and launch form) the calling thread's last launch ran, as the library recorded it."""
+    return (lib().fg_last_kernel() or b"").decode()
 
 
 def check(status: int, what: str) -> None:

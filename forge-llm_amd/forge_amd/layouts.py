@@ -626,6 +626,59 @@ def quantize_w8_rtn(w: torch.Tensor, group_size: int = -1,
     return q.to(torch.int8).contiguous(), s.to(scale_dtype)
 
 
+# ================================================================================================ W8A8 weights (host)
+# Host-side producers of the W8A8 weight formats, for checkpoints quantised on the CPU before they reach the GPU
+# (the reference builds both packed kinds from a dense CPU nn.Linear, forge/kernels/ops_gemm.py:391-393,945).  Every
+# step is an IEEE fp32 operation done the way the device quantisers do it (fg_quant.hip): scale = amax / fmax by true
+# division with a tensor divisor, 1 where `amax > 0` is false (all-zero groups and NaN-poisoned ones), codes from
+# x / scale by true division, so a weight quantised here or on the GPU has the same codes and scales bit for bit.
+_E4M3_MAX = 448.0
+
+
+def _amax_scale(amax: torch.Tensor, fmax: float) -> torch.Tensor:
+    return torch.where(amax > 0, amax / torch.full_like(amax, fmax), torch.ones_like(amax))
+
+
+def quantize_fp8_weight(w: torch.Tensor, granularity: str = "per_channel",
+                        block: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """OCP e4m3fn weight codes ``[N, K]`` and fp32 scales: ``per_tensor`` ``[1]``, ``per_channel`` ``[N]``, or
+    ``block2d`` ``[ceil(N/block), ceil(K/block)]`` (``forge/kernels/ref/gemm_fp8.py:43-85``); codes are
+    ``e4m3fn(clamp(w / s, -448, 448))``, rounded to nearest even."""
+    if w.dim() != 2:
+        raise ConfigError("w must be [N, K]")
+    if granularity not in ("per_tensor", "per_channel", "block2d"):
+        raise ConfigError(f"unknown fp8 weight granularity {granularity!r}")
+    wf = w.detach().float()
+    n, k = wf.shape
+    if granularity == "per_channel":
+        s = _amax_scale(wf.abs().amax(dim=1) if k else wf.new_zeros(n), _E4M3_MAX)
+        full = s[:, None]
+    elif granularity == "per_tensor":
+        s = _amax_scale(wf.abs().amax().reshape(1) if wf.numel() else wf.new_zeros(1), _E4M3_MAX)
+        full = s.reshape(1, 1)
+    else:
+        if block <= 0:
+            raise ConfigError(f"block must be positive, got {block}")
+        nb, kb = ceil_div(n, block), ceil_div(k, block)
+        tiles = wf.new_zeros((nb * block, kb * block))
+        tiles[:n, :k] = wf  # zero padding changes no tile's absolute max
+        s = _amax_scale(tiles.view(nb, block, kb, block).abs().amax(dim=(1, 3)), _E4M3_MAX)
+        full = s.repeat_interleave(block, 0).repeat_interleave(block, 1)[:n, :k]
+    q = (wf / full).clamp(-_E4M3_MAX, _E4M3_MAX).to(torch.float8_e4m3fn)
+    return q.contiguous(), s.contiguous()
+
+
+def quantize_int8_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-channel int8 weight codes ``[N, K]`` and fp32 scales ``[N]`` (``forge/kernels/ref/gemm_int8.py
+    :17-35`` with ``per_channel``): ``s = amax / 127``, ``q = clamp(round_half_even(w / s), -127, 127)``."""
+    if w.dim() != 2:
+        raise ConfigError("w must be [N, K]")
+    wf = w.detach().float()
+    s = _amax_scale(wf.abs().amax(dim=1) if wf.shape[1] else wf.new_zeros(wf.shape[0]), 127.0)
+    q = torch.round(wf / s[:, None]).clamp(-127, 127)
+    return torch.nan_to_num(q, nan=0.0).to(torch.int8).contiguous(), s.contiguous()
+
+
 # ================================================================================================ simple int4
 SIMPLE_LAYOUT_ID = "forge.simple.v1"
 
@@ -762,7 +815,7 @@ __all__ = [
     "PackedW4", "PackedW8", "SIMPLE_LAYOUT_ID", "cached_group_sort", "cdna4_layout", "ceil_div", "dequantize_w8_parts",
     "effective_group", "fragment_layout", "fragment_tile_perm", "get_layout", "known_layouts", "num_groups",
     "pack_nibbles_int32", "pack_simple_int4", "pack_w4", "pack_w4_from_simple", "pack_w8", "portable_layout",
-    "quantize_w4_rtn", "quantize_w8_rtn", "register_layout", "repack", "require_portable", "roundup",
+    "quantize_fp8_weight", "quantize_int8_weight", "quantize_w4_rtn", "quantize_w8_rtn", "register_layout", "repack", "require_portable", "roundup",
     "sort_columns_by_group", "unpack_nibbles_int32", "unpack_simple_int4", "unpack_w4", "unpack_w8",
     "w4_storage_shapes",
 ]

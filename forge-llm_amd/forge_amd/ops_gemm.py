@@ -44,6 +44,8 @@ from .layouts import (
     num_groups,
     pack_w4,
     pack_w8,
+    quantize_fp8_weight,
+    quantize_int8_weight,
     quantize_w4_rtn,
     quantize_w8_rtn,
     repack,
@@ -76,6 +78,12 @@ def kernel_strict() -> bool:
 def last_path(op: str) -> str | None:
     """The path the last call of ``op`` took: ``"hip"`` (or None before the first call)."""
     return _PATHS.get(op)
+
+
+def last_kernel() -> str:
+    """The kernel, with its launch form, that this thread's last op ran (``fg_last_kernel``): finer than
+    :func:`last_path`, which names the path only."""
+    return _lib.last_kernel()
 
 
 def reset_failure_memo() -> None:
@@ -602,8 +610,23 @@ def quantize_act_fp8(x: torch.Tensor, *, granularity: str = "per_token", block: 
 
 def quantize_weight_fp8(w: torch.Tensor, granularity: str = "per_channel",
                         block: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
-    """Offline FP8 weight quantisation on the GPU: per_tensor | per_channel | block2d -> ``(w_fp8 [N, K], scale)``."""
+    """Offline FP8 weight quantisation: per_tensor | per_channel | block2d -> ``(w_fp8 [N, K], scale)``.  A weight on
+    the GPU goes through the device quantiser; one on the host (a checkpoint quantised before ``.to("cuda")``) through
+    ``layouts.quantize_fp8_weight``, which gives the same codes and scales bit for bit."""
+    if not w.is_cuda:
+        if granularity not in _FP8_SCALE_SHAPES:
+            raise ConfigError(f"unknown fp8 weight granularity {granularity!r}: use {sorted(_FP8_SCALE_SHAPES)}")
+        return quantize_fp8_weight(w.reshape(-1, w.shape[-1]), granularity, block)
     return quantize_act_fp8(w, granularity=granularity, block=block)
+
+
+def quantize_weight_int8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel symmetric int8 weight quantisation -> ``(w_int8 [N, K], scale fp32 [N])``: the device
+    per-token quantiser for a weight on the GPU (one row per channel), ``layouts.quantize_int8_weight`` on the host;
+    both give the same codes and scales bit for bit."""
+    if not w.is_cuda:
+        return quantize_int8_weight(w.reshape(-1, w.shape[-1]))
+    return quantize_act_int8(w)
 
 
 def _mm_config(config: dict[str, Any] | None) -> _lib.MMConfig | None:
@@ -936,6 +959,16 @@ class KernelFp8Linear(_PackedLinear):
                 mod.bias.copy_(linear.bias.detach())
         return mod
 
+    def dequantize(self, dtype: torch.dtype | None = None) -> torch.Tensor:
+        """``codes * scale`` as a dense ``[N, K]`` weight (scales broadcast per tensor, channel or block)."""
+        n, k = self.out_features, self.in_features
+        s = self.weight_scale.float()
+        if self.granularity == "block2d":
+            s = s.repeat_interleave(self.block, 0).repeat_interleave(self.block, 1)[:n, :k]
+        else:
+            s = s.reshape(-1, 1)
+        return (self.weight_fp8.float() * s).to(dtype or torch.float32)
+
     def quant_spec(self) -> dict[str, Any]:
         return {"granularity": self.granularity, "block": self.block}
 
@@ -957,12 +990,15 @@ class KernelInt8Linear(_PackedLinear):
     def from_dense(cls, linear: nn.Linear, **_: Any) -> KernelInt8Linear:
         mod = cls(linear.in_features, linear.out_features, linear.bias is not None, linear.weight.dtype,
                   linear.weight.device)
-        q, s = quantize_act_int8(linear.weight.detach())  # one scale per output channel = per row of W
+        q, s = quantize_weight_int8(linear.weight.detach())  # one scale per output channel = per row of W
         mod._fill({"weight_int8": q, "weight_scale": s}, None)
         if linear.bias is not None:
             with torch.no_grad():
                 mod.bias.copy_(linear.bias.detach())
         return mod
+
+    def dequantize(self, dtype: torch.dtype | None = None) -> torch.Tensor:
+        return (self.weight_int8.float() * self.weight_scale.float().reshape(-1, 1)).to(dtype or torch.float32)
 
     def _linear(self, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         return int8_linear(x, self.weight_int8, self.weight_scale, bias)
@@ -995,6 +1031,6 @@ def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: Pa
 __all__ = [
     "KernelFp8Linear", "KernelInt8Linear", "KernelW4A16Linear", "KernelW8A16Linear", "PACKED_LINEAR_CLASSES",
     "device_selftest", "force_ref", "forced_impl", "fp8_linear", "int8_gemm", "int8_linear", "kernel_debug",
-    "kernel_strict", "last_path", "make_packed_linear", "prepare_fp8_scales", "prepare_w4", "quantize_act_fp8",
-    "quantize_act_int8", "quantize_weight_fp8", "reset_failure_memo", "w4_dequant", "w4a16_linear", "w8a16_linear",
+    "kernel_strict", "last_kernel", "last_path", "make_packed_linear", "prepare_fp8_scales", "prepare_w4", "quantize_act_fp8",
+    "quantize_act_int8", "quantize_weight_fp8", "quantize_weight_int8", "reset_failure_memo", "w4_dequant", "w4a16_linear", "w8a16_linear",
 ]

@@ -235,6 +235,13 @@ const char* fg_version(void);
 const char* fg_last_error(void);
 int fg_device_ok(int device);
 
+/* Name of the kernel, with its launch form, that the calling thread's last successful launch through this library
+ * ran, e.g. "w4_gemv_split_kernel<1,1,8>" or "w4_ring_kernel KS=4 + w4_ring_reduce_kernel"; "" before the first.
+ * The reference records the path each op took (last_path, forge/kernels/ops_gemm.py:81-99, and the bench's per-case
+ * `path`, forge/kernels/bench.py:188,648); this names the kernel below that path.  Valid until the same thread's next
+ * call into the library. */
+const char* fg_last_kernel(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,7 +23,7 @@ def test_header_declares_the_expected_entry_points():
     syms = declared_symbols()
     for s in ("fg_w4a16_gemm", "fg_w4a16_workspace_bytes", "fg_w4_dequant", "fg_int8_gemm", "fg_fp8_gemm",
               "fg_quant_int8_rowwise", "fg_quant_fp8_rowwise", "fg_quant_fp8_block", "fg_version", "fg_last_error",
-              "fg_device_ok"):
+              "fg_device_ok", "fg_last_kernel"):
         assert s in syms
 
 

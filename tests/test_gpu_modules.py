@@ -96,3 +96,42 @@ def test_int8_module_forward_is_exact(m):
     fresh = ops.make_packed_linear("int8", in_features=k, out_features=n, bias=torch.zeros(n), device=DEV)
     fresh.load_state_dict(mod.state_dict())
     assert torch.equal(fresh(x.to(DEV)), y)
+
+
+@pytest.mark.parametrize("kind,kw", [("fp8", {"granularity": "per_channel"}), ("fp8", {"granularity": "per_tensor"}),
+                                     ("fp8", {"granularity": "block2d", "block": 128}), ("int8", {})])
+def test_w8a8_module_quantised_on_host_then_moved(kind, kw):
+    """A checkpoint quantised on the CPU, then moved to the GPU (the reference's flow): its codes and scales equal
+    the device quantisers' bit for bit, and its forward matches the same module built on the GPU bit for bit."""
+    n, k = 384, 1024
+    lin = torch.nn.Linear(k, n)
+    with torch.no_grad():
+        lin.weight.mul_(0.5)
+        lin.weight[5] = 0.0
+    host = ops.make_packed_linear(kind, lin, **kw)
+    assert all(not t.is_cuda for t in host.state_dict().values())
+    moved = host.to(DEV)
+    dev_mod = ops.make_packed_linear(kind, torch.nn.Linear(k, n).to(DEV).requires_grad_(False), **kw)
+    with torch.no_grad():
+        dev_mod.weight_scale.zero_()
+        dev_mod.bias.copy_(lin.bias.detach().to(DEV))
+    if kind == "fp8":
+        qd, sd = ops.quantize_weight_fp8(lin.weight.detach().to(DEV), kw["granularity"], kw.get("block", 128))
+        assert torch.equal(moved.weight_fp8.view(torch.uint8), qd.view(torch.uint8))
+        assert torch.equal(moved.weight_scale, sd.reshape(moved.weight_scale.shape))
+        with torch.no_grad():
+            dev_mod.weight_fp8.copy_(qd)
+            dev_mod.weight_scale.copy_(sd.reshape(dev_mod.weight_scale.shape))
+    else:
+        qd, sd = ops.quantize_weight_int8(lin.weight.detach().to(DEV))
+        assert torch.equal(moved.weight_int8, qd) and torch.equal(moved.weight_scale, sd)
+        with torch.no_grad():
+            dev_mod.weight_int8.copy_(qd)
+            dev_mod.weight_scale.copy_(sd)
+    x = x_act(33, k, torch.bfloat16, seed=9).to(DEV)
+    y = moved(x)
+    assert torch.equal(y, dev_mod(x))
+    assert ops.last_path(f"{kind}_linear") == "hip"
+    fresh = ops.make_packed_linear(kind, in_features=k, out_features=n, bias=torch.zeros(n), device=DEV, **kw)
+    fresh.load_state_dict(host.state_dict())
+    assert torch.equal(fresh(x), y)

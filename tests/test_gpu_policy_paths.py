@@ -16,12 +16,13 @@ import torch
 from forge_amd import layouts as L
 from forge_amd import ops_gemm as ops
 from oracle import gemm as og
+from oracle import w4 as ow
 from tests._util import assert_close, gen, oracle_packed, to_f32, w4_parts, x_act
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 ODT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
-LLAMA = {"qkv": (4096, 6144), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
+LLAMA = {"qkv": (4096, 6144), "o_proj": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)}  # (K, N)
 
 
 def _rows_oracle(xs: list[torch.Tensor], packed: dict) -> list[np.ndarray]:
@@ -62,7 +63,7 @@ def test_w4_policy_33_to_64_rows_full_size(shape):
 def test_w4_policy_13_to_32_rows_full_size(shape):
     """17..32 rows (13..16 over gate+up's 28672 channels): the policy runs the LDS-ring kernel on portable_row
     weights; forcing impl=mfma runs the skinny kernel.  Both against the oracle, the policy's result reproducible."""
-    k, n = {"o_proj": (4096, 4096), **LLAMA}[shape]
+    k, n = LLAMA[shape]
     q, s_, z = w4_parts(n, k, 128, False, seed=k + n + 1)
     p = L.pack_w4(q, s_, z, 128).to(DEV)
     cases = [(17, torch.bfloat16, True), (24, torch.float16, False), (32, torch.bfloat16, False)]
@@ -156,3 +157,53 @@ def test_int8_configs4_shapes_exact(m, k, n):
     assert np.array_equal(acc[rows].cpu().numpy(), ref_acc)
     ref = og.int8_gemm_ref(xq, sa[rows].cpu().numpy(), wq, sw.cpu().numpy(), None, acc=ref_acc)
     assert torch.equal(y[rows].cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------------------------- configs[2] prefill
+_PREFILL_CACHE: dict = {}
+
+
+def _prefill_weights(shape: str, bits: int):
+    """One weight per (shape, bits) for every M of the prefill cells: the packed GPU copy and the oracle's fp32
+    dequantised ``[N, K]`` (rows of x times its transpose are the oracle's rows of y)."""
+    key = (shape, bits)
+    if key not in _PREFILL_CACHE:
+        if any(sh != shape for sh, _ in _PREFILL_CACHE):
+            _PREFILL_CACHE.clear()  # one shape at a time: gate+up's dequantised oracle weight is 470 MB per format
+        k, n = LLAMA[shape]
+        if bits == 4:
+            q, s, z = w4_parts(n, k, 128, False, seed=2 * k + n)
+            packed = L.pack_w4(q, s, z, 128).to(DEV)
+            dense = ow.dequantize_parts(q.numpy(), s.float().numpy(), z.numpy(), 128)
+        else:
+            g = gen(3 * k + n)
+            q = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+            s = (torch.rand(n, k // 128, generator=g) * 0.018 + 0.002).half()
+            packed = L.pack_w8(q, s, 128).to(DEV)
+            dense = og.dequantize_w8(og.pack_w8(q.numpy(), s.float().numpy(), 128))
+        _PREFILL_CACHE[key] = (packed, dense)
+    return _PREFILL_CACHE[key]
+
+
+PREFILL_CELLS = [(m, sh) for sh in ("qkv", "o_proj", "gate_up", "down") for m in (512, 2048, 8192)]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("m,shape", PREFILL_CELLS)
+def test_prefill_policy_configs2_cells(m, shape, bits):
+    """M in {512, 2048, 8192} on the four Llama-3-8B shapes through the automatic policy (bf16 x ~ N(0,1),
+    group 128; W4 asymmetric with zero-points U{6..9}, W8A16 symmetric int8).  Rows sampled from the first, middle
+    and last row tiles are checked against the oracle over all N columns, within the north-star bar plus compare();
+    the result is reproducible run to run."""
+    k, n = LLAMA[shape]
+    packed, dense = _prefill_weights(shape, bits)
+    x = x_act(m, k, torch.bfloat16, seed=m + k + n + bits)
+    xd = x.to(DEV)
+    op = ops.w4a16_linear if bits == 4 else ops.w8a16_linear
+    y = op(xd, packed)
+    assert ops.last_path("w4a16_linear" if bits == 4 else "w8a16_linear") == "hip"
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    rows = sorted({0, 1, 127, 128, m // 2 + 5, m - 129, m - 2, m - 1})
+    ref = (to_f32(x[rows]) @ dense.T).astype(np.float32)
+    assert_close(y[rows].cpu(), ref, "bfloat16", what=f"w{bits} prefill {shape} m={m}")
+    assert torch.equal(y, op(xd, packed)), f"w{bits} {shape} m={m}: not reproducible"

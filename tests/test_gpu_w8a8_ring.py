@@ -103,8 +103,10 @@ def test_ring_config_rejects():
 
 @pytest.mark.parametrize("m,k,n", [(1, 8192, 10240), (64, 8192, 10240), (64, 28672, 8192), (64, 8192, 57344)])
 def test_ring_int8_config_sizes_policy(m, k, n):
-    """configs[4] at small M: the policy's kernel (the ring kernel, 64-row tiles) equals the 64 x 64 instance bit for bit
-    and the oracle on sampled rows (bf16 output, per-token x per-channel scales, bias)."""
+    """configs[4] at small M: the policy's kernel (the INT8 decode GEMV at M = 1, the ring kernel's 64-row tiles at
+    M = 64, and at M = 64 over N = 57344 the 256-row kernel, whose 224 tiles reach 5/8 of the CUs) equals the forced
+    64 x 64 ring instance bit for bit and the oracle on sampled rows (bf16 output, per-token x per-channel scales,
+    bias)."""
     g = torch.Generator(device=DEV).manual_seed(m + k + n)
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=DEV, generator=g)
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=DEV, generator=g)
@@ -112,6 +114,9 @@ def test_ring_int8_config_sizes_policy(m, k, n):
     sw = torch.rand(n, device=DEV, generator=g) * 0.01 + 0.001
     b = torch.randn(n, device=DEV, generator=g)
     y = ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16)
+    kern = ops.last_kernel()
+    expect = "int8_gemv_kernel" if m == 1 else ("mm_big_kernel" if n == 57344 else "mm_ring_kernel 64x")
+    assert kern.startswith(expect), kern
     y64 = ops.int8_gemm(a, sa, w, sw, b, out_dtype=torch.bfloat16, config={"tile_m": 64, "tile_n": 64})
     assert torch.equal(y, y64)
     rows = sorted({0, m // 2, m - 1})

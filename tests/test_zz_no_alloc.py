@@ -37,21 +37,28 @@ def _both(m, n, k, seed, cfg=None):
     y_ws = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     y_na = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
     _lib.check(lib.fg_w4a16_gemm(*_args(x, p, y_ws, cfg), _lib.ptr(ws), ws_bytes, stream), "fg_w4a16_gemm")
+    kern_ws = _lib.last_kernel()
     _lib.check(lib.fg_w4a16_gemm_noalloc(*_args(x, p, y_na, cfg), stream), "fg_w4a16_gemm_noalloc")
+    assert _lib.last_kernel() == kern_ws, "both entry points must run the same kernels"
     torch.cuda.synchronize()
-    return y_ws, y_na
+    return y_ws, y_na, kern_ws
 
 
 def test_noalloc_matches_workspace_entry_point_twice():
-    # 64 rows over gate+up: 64-row prefill tiles with 2 K splits (14.7 MB of partials in the scratch buffer)
-    y_ws, y_na = _both(64, 28672, 4096, seed=1)
+    # 64 rows over down (K = 14336): the LDS-ring kernel with 8 K splits, whose 8.4 MB of fp32 partials go to the
+    # scratch buffer and are summed by its reduce kernel
+    y_ws, y_na, kern = _both(64, 4096, 14336, seed=1)
+    assert "w4_ring_kernel" in kern and "KS=8" in kern and "reduce" in kern, kern
     assert torch.equal(y_ws, y_na)
-    # then a smaller problem (40 rows over qkv, 8 K splits, 7.9 MB): the first call's partials stay behind it
-    y_ws, y_na = _both(40, 6144, 4096, seed=2)
+    # then a smaller problem (40 rows over qkv: the ring kernel with 4 K splits, 3.9 MB): the first call's partials
+    # stay behind it in the buffer
+    y_ws, y_na, kern = _both(40, 6144, 4096, seed=2)
+    assert "w4_ring_kernel" in kern and "reduce" in kern, kern
     assert torch.equal(y_ws, y_na)
     # and a forced split count through the tiled MFMA kernel's split-K path
     cfg = _lib.W4Config(_lib.W4_MFMA, 0, 0, 32, 4)
-    y_ws, y_na = _both(24, 2048, 4096, seed=3, cfg=cfg)
+    y_ws, y_na, kern = _both(24, 2048, 4096, seed=3, cfg=cfg)
+    assert "w4_mfma_kernel splits=4" in kern, kern
     assert torch.equal(y_ws, y_na)
 
 
