@@ -33,6 +33,26 @@ void w4_mfma_split_plan(int M, int N, int K, int tile_m, int split_k, int* kchun
 bool w4_big_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, int64_t K, int gs,
                int64_t G);
 size_t w4_big_workspace_bytes(int M, int N, int K, int split_k, bool w8);
+bool w4_pc_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, const void* scales,
+              int sdt, int64_t lds, int64_t N, int64_t K, int gs, int64_t G);
+size_t w4_pc_workspace_bytes(int M, int N, int K, int split_k);
+bool w4_pp_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const int32_t* perm, const void* scales,
+              int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, int64_t M, int64_t N, int64_t K, int gs,
+              int64_t G);
+bool w8_pp_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+              int64_t M, int64_t N, int64_t K, int gs, int64_t G);
+size_t w4_pp_workspace_bytes(int M, int N, int K, int split_k);
+hipError_t launch_w4_pp(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                        int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                        int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
+                        hipStream_t s);
+hipError_t launch_w8_pp(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq, const void* scales,
+                        int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, float* ws, int M, int N,
+                        int K, int gs, bool single_group, int split_k, hipStream_t s);
+hipError_t launch_w4_pc(const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq, const void* scales,
+                        int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                        int64_t ldy, float* ws, int M, int N, int K, int gs, bool single_group, int split_k,
+                        hipStream_t s);
 bool w8a16_skinny_ok(const void* x, int64_t ldx, const int8_t* qw, int64_t ldq, int sdt, int64_t lds, int64_t M,
                      int64_t N, int64_t K, int gs, int64_t G);
 hipError_t launch_w8a16_skinny(const void* x, int64_t ldx, bool xbf16, const int8_t* qw, int64_t ldq,
@@ -80,17 +100,6 @@ bool int8_gemv_ok(const void* a, int64_t lda, const void* b, int64_t ldb, int64_
 hipError_t launch_int8_gemv(const int8_t* a, int64_t lda, const float* sa, int64_t sa_len, const int8_t* b,
                             int64_t ldb, const float* sb, int64_t sb_len, const void* bias, int bdt, void* y,
                             int64_t ldy, int ydt, int M, int N, int K, hipStream_t s);
-size_t libgemm_workspace_bytes(int N, int K);
-bool libgemm_ok(int xdt, const void* x, const void* bias, int bdt, const void* y, int64_t M, int64_t N, int64_t K,
-                int64_t ldx, int64_t ldy, hipStream_t s);
-hipError_t launch_w4_libgemm(const void* x, int64_t ldx, int xdt, const int32_t* qw, int64_t ldq, const void* scales,
-                             int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const int32_t* g_idx,
-                             const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K, int gs,
-                             void* ws, size_t ws_bytes, hipStream_t s);
-bool w8_dequant16_ok(const int8_t* qw, int64_t ldq, int odt, int64_t K, int gs, int64_t G);
-hipError_t launch_w8a16_libgemm(const void* x, int64_t ldx, int xdt, const int8_t* qw, int64_t ldq, const void* scales,
-                                int sdt, int64_t lds, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
-                                int K, int gs, void* ws, size_t ws_bytes, hipStream_t s);
 size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K);
 hipError_t launch_w4_ring(bool portable, const void* x, int64_t ldx, bool xbf16, const int32_t* qw, int64_t ldq,
                           const void* scales, int sdt, int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias,
@@ -276,22 +285,6 @@ namespace {
 // kernel: measured on the Llama-3-8B shapes, the skinny kernel wins up to 32 rows (and to 64 rows for N, K <= 4096),
 // the prefill kernel from 48 rows (gate+up at M = 64: 1.10 against 0.60 TB/s).
 constexpr int64_t kPrefillMinM = 33;
-// Rows from which the policy takes the dequantise + library GEMM route (when the caller's workspace can hold it): the
-// dequantisation costs 2.5 N K bytes once, the fused kernel loses a share of every MFMA cycle.  Graph replays over four
-// distinct weights, us, fused / dequantise + GEMM: M = 1024 qkv 87.9 / 72.9, o_proj 65.0 / 56.8, down 177 / 172,
-// gate+up 261 / 278; M = 2048 127 / 104, 93 / 77, 297 / 248, 494 / 438; M = 8192 408 / 310, 282 / 203, 844 / 645,
-// 1711 / 1302.  With the wavefront-per-2048-columns dequantisation the route moved ahead from 768 rows on every shape
-// (M = 768: qkv 86 / 62, o_proj 59 / 46, gate+up 249 / 209, down 153 / 132; gate+up M = 1024 253 / 242); at M = 512
-// the fused kernel stays ahead but for qkv (o_proj 40 / 43, gate+up 141 / 160, down 89 / 113, qkv 60 / 54).
-int64_t dequant_gemm_min_m(int64_t, int64_t) { return 768; }
-
-// W8A16 rows from which the policy takes the same route (int8 weights dequantised by w8_dequant16_kernel, 3 N K bytes)
-// over the fused prefill kernel.  Graph replays over four distinct weights, us, fused / route: M = 768 qkv 86.9 / 62.4,
-// o_proj 63.1 / 44.8, gate+up 251 / 210, down 179 / 130; M = 2048 124 / 97, 97 / 72, 498 / 409, 317 / 224; M = 8192
-// 415 / 300, 280 / 194, 1807 / 1286, 907 / 640; at M = 512 the fused kernel stays ahead on gate+up (141 / 155) and
-// down (111 / 120).
-int64_t w8a16_dequant_gemm_min_m(int64_t, int64_t) { return 768; }
-
 // Whether the automatic policy sends a 4..64-row call to the LDS-ring kernel (portable_row weights): 17..64 rows,
 // 4..16 over N >= 16384 and 9..16 over K >= 8192 (fg::w4_ring_preferred; measured on the Llama-3-8B shapes, us, ring
 // / previous choice: M = 64 qkv 17.8 / 22.4, o_proj 15.1 / 20.4, gate+up 37.8 / 51.3, down 25.4 / 32.6; M = 32
@@ -302,6 +295,38 @@ bool ring_policy(const fg_w4_config* cfg, int64_t M, int64_t N, int64_t K) {
          K % 128 == 0 && fg::w4_ring_preferred(true, (int)M, (int)N, (int)K);
 }
 
+// Prefill kernel among those whose conditions hold (pp: ping-pong 256 x 256, pc: producer / consumer 256 x 128, big:
+// the all-rounder), 2 / 4 / 5 as in the launch switch; 1 (skinny) when `skinny_first`.  tile_n = 256 / 128 / 64
+// forces ping-pong / producer-consumer / all-rounder.  Otherwise from 256 rows: the ping-pong kernel once its tiles
+// come near one per CU (>= 160 of 256 x 256), else the producer / consumer kernel (graph replays over four distinct
+// weights, us, ping-pong / producer-consumer / all-rounder: M = 512 qkv 53.0 / 50.4 / 60.5, o_proj 48.1 / 36.9 / 40.9,
+// gate+up 114.6 / 138.6 / 135.1, down 87.4 / 75.0 / 96.9; M = 2048 qkv 108.9 / 135.2 / 131.0, o_proj 98.3 / 78.4 /
+// 93.4, gate+up 449.5 / 501.7 / 502.3, down 234.8 / 232.5 / 297.4; M = 8192 qkv 367 / 434 / 413, o_proj 246 / 294 /
+// 273, gate+up 1624 / 1916 / 1799, down 779 / 894 / 878); below 256 rows the all-rounder.
+constexpr int64_t kPpMinTiles = 160;
+int64_t pp_tiles(int64_t M, int64_t N) { return ((M + 255) / 256) * ((N + 255) / 256); }
+int prefill_kernel(int tile_n, int64_t M, int64_t N, bool pp, bool pc, bool big, bool skinny_first) {
+  if (tile_n == 256 && pp) return 5;
+  if (tile_n == 128 && pc) return 4;
+  if (tile_n == 64 && big) return 2;
+  if (skinny_first) return 1;
+  if (M >= 256 && pp && pp_tiles(M, N) >= kPpMinTiles) return 5;
+  if (M >= 256 && pc) return 4;
+  return big ? 2 : 0;
+}
+
+// Split-K workspace of the prefill kernel prefill_kernel picks for this shape and tile_n, and of those it falls back to
+// when the operands rule a kernel out at launch (the ping-pong kernel falls back to the producer / consumer kernel,
+// W4 only, and both to the all-rounder).
+size_t prefill_workspace_bytes(int tile_n, int64_t M, int64_t N, int64_t K, int split_k, bool w4) {
+  const bool pp = tile_n == 256 || (tile_n == 0 && M >= 256 && pp_tiles(M, N) >= kPpMinTiles);
+  const bool pc = w4 && (tile_n == 128 || tile_n == 256 || (tile_n == 0 && M >= 256));
+  size_t b = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, split_k, !w4);
+  if (pp) b = std::max(b, fg::w4_pp_workspace_bytes((int)M, (int)N, (int)K, split_k));
+  if (pc) b = std::max(b, fg::w4_pc_workspace_bytes((int)M, (int)N, (int)K, split_k));
+  return b;
+}
+
 // Kernel choice and launch shape for one W4A16 call; fg_w4a16_workspace_bytes and fg_w4a16_gemm share it so the
 // workspace a caller sizes is the workspace the launch uses.
 struct W4Plan {
@@ -309,11 +334,10 @@ struct W4Plan {
   int gemv, mt, rows, max_blocks;  // GEMV: FG_GEMV_* kernel, rows of x per pass, wave-kernel knobs
   int tile_m, splits;              // MFMA
   size_t ws_bytes;
-  bool dequant_gemm;  // AUTO with many rows: the launch takes the dequantise + library GEMM route where it applies
 };
 
 int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned, bool q_aligned, bool has_g_idx,
-            const fg_w4_config* cfg, bool allow_dequant_gemm, W4Plan* p) {
+            const fg_w4_config* cfg, W4Plan* p) {
   const int gs = group_size > 0 ? group_size : (int)K;
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
   const int G = (int)((K + gs - 1) / gs);
@@ -334,7 +358,9 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
   const bool mfma_ok = !has_g_idx && q_aligned && x_aligned && (K % 8 == 0);
   // the prefill kernel's shape conditions (an act-order perm, known only at launch, sends the call to MFMA instead)
   const bool prefill_ok = mfma_ok && (K % 64 == 0) && (gs % 32 == 0 || G == 1);
-  int use = impl;
+  // FG_W4_DEQUANT_GEMM (the reference's dequant_matmul) names the prefill kernels: they dequantise tiles into LDS and
+  // feed them to bf16 / fp16 MFMA, the two steps of that route fused
+  int use = impl == FG_W4_DEQUANT_GEMM ? FG_W4_PREFILL : impl;
   if (use == FG_W4_AUTO)
     use = gemv_ok ? FG_W4_GEMV : (prefill_ok && M >= kPrefillMinM ? FG_W4_PREFILL : (mfma_ok ? FG_W4_MFMA : FG_W4_GENERIC));
   if (use == FG_W4_PREFILL && !prefill_ok)
@@ -346,24 +372,9 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
   if (use == FG_W4_MFMA && !mfma_ok)
     return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: MFMA path needs no g_idx, K%%8==0, ldq%%4==0, ldx%%8==0 and "
                                  "16-byte aligned x/qweight");
-  if (use == FG_W4_DEQUANT_GEMM && !allow_dequant_gemm)
-    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm_noalloc: the dequantise + library GEMM route needs a caller workspace");
-  if (use == FG_W4_DEQUANT_GEMM && K % 8 != 0)
-    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs K %% 8 == 0");
-  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC && use != FG_W4_PREFILL &&
-      use != FG_W4_DEQUANT_GEMM)
+  if (use != FG_W4_GEMV && use != FG_W4_MFMA && use != FG_W4_GENERIC && use != FG_W4_PREFILL)
     return fail(FG_EINVAL, "fg_w4a16_gemm: unknown impl %d", impl);
-  *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0, false};
-  // many rows under the policy: the launch takes the dequantise + library GEMM route if the operands allow it (16-bit
-  // x, the bias type, no perm), else the kernel chosen above; the workspace covers both
-  const bool dq_auto = impl == FG_W4_AUTO && allow_dequant_gemm && M >= dequant_gemm_min_m(N, K) && K % 8 == 0 &&
-                       (use == FG_W4_PREFILL || use == FG_W4_MFMA || use == FG_W4_GENERIC) &&
-                       !(cfg && (cfg->tile_m || cfg->split_k));
-  if (use == FG_W4_DEQUANT_GEMM || dq_auto) {
-    p->dequant_gemm = true;
-    p->ws_bytes = fg::libgemm_workspace_bytes((int)N, (int)K);
-    if (use == FG_W4_DEQUANT_GEMM) return FG_OK;
-  }
+  *p = W4Plan{use, gemv, mt, 4, 0, 0, 1, 0};
   if (use == FG_W4_GEMV) {
     p->rows = cfg && cfg->rows_per_wave ? cfg->rows_per_wave : 4;
     if (p->rows != 1 && p->rows != 2 && p->rows != 4) return fail(FG_EINVAL, "fg_w4a16_gemm: rows_per_wave must be 1, 2 or 4");
@@ -378,7 +389,7 @@ int plan_w4(int64_t M, int64_t N, int64_t K, int32_t group_size, bool x_aligned,
     // the launch picks among the skinny, prefill and tiled MFMA kernels once the operand addresses are known (an
     // act-order perm or misaligned operands rule some out): size the workspace for either split-K kernel
     if (prefill_ok) {
-      const size_t wb = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, p->splits, false);
+      const size_t wb = prefill_workspace_bytes(cfg ? cfg->tile_n : 0, M, N, K, p->splits, true);
       if (wb > p->ws_bytes) p->ws_bytes = wb;
     }
     // ... and for the LDS-ring kernel when the policy sends the call there
@@ -398,7 +409,7 @@ size_t fg_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
                                 int32_t q_aligned, int32_t has_g_idx, const fg_w4_config* cfg) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
   W4Plan p;
-  if (plan_w4(M, N, K, group_size, x_aligned != 0, q_aligned != 0, has_g_idx != 0, cfg, true, &p) != FG_OK) return 0;
+  if (plan_w4(M, N, K, group_size, x_aligned != 0, q_aligned != 0, has_g_idx != 0, cfg, &p) != FG_OK) return 0;
   return p.ws_bytes;
 }
 
@@ -433,7 +444,7 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   const bool x_aligned = (ldx % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
   const bool q_aligned = (ldq % 4 == 0) && (reinterpret_cast<uintptr_t>(qweight) % 16 == 0);
   W4Plan p;
-  const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, !static_ws, &p);
+  const int rc = plan_w4(M, N, K, group_size, x_aligned, q_aligned, g_idx != nullptr, cfg, &p);
   if (rc != FG_OK) return rc;
   if (static_ws && p.ws_bytes > workspace_bytes)
     return fail(FG_EINVAL, "fg_w4a16_gemm_noalloc: this launch needs %zu bytes of split-K scratch, the library's static "
@@ -446,19 +457,6 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool xbf16 = x_dtype == FG_BF16;
   hipError_t e;
-  if (p.dequant_gemm) {
-    const bool fits = perm == nullptr && fg::libgemm_ok(x_dtype, x, bias, bias_dtype, y, M, N, K, ldx, ldy, s) &&
-                      reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
-    if (fits)
-      return hip_status(fg::launch_w4_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, zeros, ldz,
-                                              g_idx, bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, workspace,
-                                              workspace_bytes, s),
-                        "fg_w4a16_gemm dequantise + library GEMM");
-    if (p.impl == FG_W4_DEQUANT_GEMM)
-      return fail(FG_EUNSUPPORTED, "fg_w4a16_gemm: the dequantise + library GEMM route needs no act-order perm, x and "
-                                   "y with 16-byte aligned rows, a bias in fp32 or x's dtype, a 256-byte aligned "
-                                   "workspace and, under graph capture, a first call of the same problem outside it");
-  }
   // 3-4 rows over weights larger than 4096 x 4096: the skinny MFMA kernel where it applies (it needs no workspace).
   // Measured at M = 4 (us): qkv 8.2 against 8.7 for the GEMV, gate+up 20.5 against 22.8, down 14.8 against 16.2;
   // o_proj (4096 x 4096) 6.8 against 6.1 stays on the GEMV, as do 1-2 rows.
@@ -491,9 +489,17 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
                         fg::w4_skinny_ok(x, ldx, qweight, ldq, perm, scale_dtype, lds, zeros ? ldz : 0, (int)M, N, K,
                                          gs, G);
     const bool big = fg::w4_big_ok(x, ldx, qweight, ldq, perm, K, gs, G) && !(cfg && cfg->tile_m);
-    int kern = 0;  // 0: LDS-tiled MFMA, 1: skinny, 2: prefill, 3: LDS ring
+    const bool pc = fg::w4_pc_ok(x, ldx, qweight, ldq, perm, scales, scale_dtype, lds, N, K, gs, G) &&
+                    !(cfg && cfg->tile_m);
+    const bool pp = fg::w4_pp_ok(x, ldx, qweight, ldq, perm, scales, scale_dtype, lds, zeros, zeros ? ldz : 0, M, N,
+                                 K, gs, G) &&
+                    !(cfg && cfg->tile_m);
+    // 0: LDS-tiled MFMA, 1: skinny, 2: all-round prefill, 3: LDS ring, 4: producer / consumer prefill, 5: ping-pong
+    // prefill
+    int kern = 0;
     if (p.impl == FG_W4_PREFILL)
-      kern = (auto_impl && skinny && M <= 64 && N <= 4096 && K <= 4096) ? 1 : (big ? 2 : 0);
+      kern = prefill_kernel(cfg ? cfg->tile_n : 0, M, N, pp, pc, big,
+                            auto_impl && skinny && M <= 64 && N <= 4096 && K <= 4096);
     else
       kern = skinny ? 1 : ((auto_impl && big) ? 2 : 0);
     if (ring_policy(cfg, M, N, K) && perm == nullptr &&
@@ -509,6 +515,12 @@ int w4a16_run(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, i
     else if (kern == 1)
       e = fg::launch_w4_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
                                ldy, (int)M, (int)N, (int)K, gs, G == 1, s);
+    else if (kern == 5)
+      e = fg::launch_w4_pp(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y, ldy,
+                           static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
+    else if (kern == 4)
+      e = fg::launch_w4_pc(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y, ldy,
+                           static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
     else if (kern == 2)
       e = fg::launch_w4_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, zeros, ldz, bias, bias_dtype, y,
                             ldy, static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, p.splits, s);
@@ -662,20 +674,12 @@ size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_s
   const int gs = group_size > 0 ? group_size : (int)K;
   const int64_t G = (K + gs - 1) / gs;
   const int impl = cfg ? cfg->impl : FG_W4_AUTO;
-  // the dequantise + library GEMM route: forced, or many rows under the policy (the launch falls back to the kernels
-  // below when the operands do not allow the route, so the workspace covers those too)
-  const bool route_shape = K % 16 == 0 && (gs % 16 == 0 || G == 1) && fg::group_div_exact(K, gs, G, 1);
-  if (impl == FG_W4_DEQUANT_GEMM) return route_shape ? fg::libgemm_workspace_bytes((int)N, (int)K) : 0;
-  const size_t route = impl == FG_W4_AUTO && route_shape && M >= w8a16_dequant_gemm_min_m(N, K) &&
-                               !(cfg && (cfg->tile_m || cfg->split_k))
-                           ? fg::libgemm_workspace_bytes((int)N, (int)K)
-                           : 0;
-  // the prefill kernel's split-K partials, whenever it may run (its alignment conditions are checked at launch)
+  // the prefill kernels' split-K partials, whenever one may run (their alignment conditions are checked at launch)
   const bool prefill_shape = (K % 64 == 0) && (gs % 32 == 0 || G == 1);
-  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return route;
+  if (!prefill_shape || impl == FG_W4_GENERIC || impl == FG_W4_MFMA || impl == FG_W4_GEMV) return 0;
   const size_t ring = impl == FG_W4_AUTO && w8a16_ring_rows(M, N, K) ? fg::w8a16_ring_workspace_bytes((int)M, (int)N, (int)K)
                                                                : 0;
-  return std::max({route, ring, fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0, true)});
+  return std::max(ring, prefill_workspace_bytes(cfg ? cfg->tile_n : 0, M, N, K, cfg ? cfg->split_k : 0, false));
 }
 
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,
@@ -694,32 +698,12 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
   if (ldq < K || lds < N || ldx < K || ldy < N) return fail(FG_EINVAL, "fg_w8a16_gemm: leading dimensions too small");
   if (n_groups < G)
     return fail(FG_EINVAL, "fg_w8a16_gemm: n_groups=%d does not cover K=%lld with group %d", n_groups, (long long)K, gs);
-  const int impl = cfg ? cfg->impl : FG_W4_AUTO;
-  if (impl != FG_W4_AUTO && impl != FG_W4_GEMV && impl != FG_W4_MFMA && impl != FG_W4_PREFILL &&
-      impl != FG_W4_GENERIC && impl != FG_W4_DEQUANT_GEMM)
-    return fail(FG_EINVAL, "fg_w8a16_gemm: unknown impl %d", impl);
+  // FG_W4_DEQUANT_GEMM names the prefill kernels, as for W4A16
+  const int impl = cfg && cfg->impl == FG_W4_DEQUANT_GEMM ? FG_W4_PREFILL : (cfg ? cfg->impl : FG_W4_AUTO);
+  if (impl != FG_W4_AUTO && impl != FG_W4_GEMV && impl != FG_W4_MFMA && impl != FG_W4_PREFILL && impl != FG_W4_GENERIC)
+    return fail(FG_EINVAL, "fg_w8a16_gemm: unknown impl %d", cfg->impl);
   const bool xbf16 = x_dtype == FG_BF16;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // many rows: dequantise + hipBLASLt's GEMM where the operands, the workspace and (under capture) an existing plan
-  // allow it; forced, it must apply
-  const bool route_auto = impl == FG_W4_AUTO && M >= w8a16_dequant_gemm_min_m(N, K) && !(cfg && (cfg->tile_m || cfg->split_k));
-  if (route_auto || impl == FG_W4_DEQUANT_GEMM) {
-    const bool fits = fg::w8_dequant16_ok(qweight, ldq, x_dtype, K, gs, G) &&
-                      fg::libgemm_ok(x_dtype, x, bias, bias_dtype, y, M, N, K, ldx, ldy, s) && workspace &&
-                      reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
-                      workspace_bytes >= fg::libgemm_workspace_bytes((int)N, (int)K);
-    if (fits)
-      return hip_status(fg::launch_w8a16_libgemm(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, bias,
-                                                 bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, workspace,
-                                                 workspace_bytes, s),
-                        "fg_w8a16_gemm dequantise + library GEMM");
-    if (impl == FG_W4_DEQUANT_GEMM)
-      return fail(FG_EUNSUPPORTED, "fg_w8a16_gemm: the dequantise + library GEMM route needs K %% 16 == 0, group %% 16 "
-                                   "== 0 (or one group), ldq %% 16 == 0, 16-byte aligned qweight, x and y with 16-byte "
-                                   "aligned rows, a bias in fp32 or x's dtype, a 256-byte aligned workspace of "
-                                   "fg_w8a16_workspace_bytes and, under graph capture, a first call of the same "
-                                   "problem outside it");
-  }
   const bool gemv = fg::w8a16_gemv_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G);
   const bool skinny = fg::w8a16_skinny_ok(x, ldx, qweight, ldq, scale_dtype, lds, M, N, K, gs, G);
   const bool big = fg::w8_big_ok(x, ldx, qweight, ldq, K, gs, G);
@@ -761,13 +745,22 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     e = fg::launch_w8a16_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
                                 (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (kern == 2) {
-    const size_t need = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, cfg ? cfg->split_k : 0, true);
+    // the ping-pong kernel or the all-rounder, by the W4A16 rule (no producer / consumer kernel for int8 weights)
+    const bool pp = fg::w8_pp_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G) &&
+                    !(cfg && cfg->tile_m);
+    const int pk = prefill_kernel(cfg ? cfg->tile_n : 0, M, N, pp, false, big, false);
+    const int split = cfg ? cfg->split_k : 0;
+    const size_t need = pk == 5 ? fg::w4_pp_workspace_bytes((int)M, (int)N, (int)K, split)
+                                : fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, split, true);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
       return fail(FG_EINVAL, "fg_w8a16_gemm: workspace of %zu bytes needed, %zu given", need,
                   workspace ? workspace_bytes : (size_t)0);
-    e = fg::launch_w8_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
-                          static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, cfg ? cfg->split_k : 0,
-                          s);
+    if (pk == 5)
+      e = fg::launch_w8_pp(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
+                           static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, split, s);
+    else
+      e = fg::launch_w8_big(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
+                            static_cast<float*>(workspace), (int)M, (int)N, (int)K, gs, G == 1, split, s);
   } else {
     e = fg::launch_w8a16_generic(x, ldx, x_dtype, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
                                  (int)M, (int)N, (int)K, gs, s);

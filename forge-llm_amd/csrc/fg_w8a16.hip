@@ -2,8 +2,8 @@
 // (symmetric, no zero-point), x bf16 / fp16.  The portable_row W8 layout: qweight int8 [N, K] row-major, scales [G, N].
 //
 // The policy (fg_w8a16_gemm) runs 17..64 rows, and 3..16 rows over N >= 16384 or K >= 8192, on the W4 LDS-ring kernel's
-// int8 form (w8a16_ring_kernel, fg_w4_ring.hip); the skinny kernel below serves the other 3..64-row calls, and from
-// 768 rows w8_dequant16_kernel (at the end of this file) feeds the dequantise + hipBLASLt route of fg_libgemm.hip.
+// int8 form (w8a16_ring_kernel, fg_w4_ring.hip); the skinny kernel below serves the other 3..64-row calls, and the
+// prefill kernels (fg_w4_big.hip, fg_w4_pp.hip) the larger ones.
 //
 // Skinny kernel (M <= 64): the W4 skinny kernel's split-K structure (a wavefront owns T tiles of 16 channels and one K
 // slice in 128-column steps; KS slices per workgroup summed in slice order through LDS; operands straight from global
@@ -531,82 +531,6 @@ hipError_t launch_w8a16_generic(const void* x, int64_t ldx, int xdt, const int8_
   note_kernel("w8a16_generic_kernel");
   hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, ldx, xdt, qw, ldq,
                      scales, sdt, lds, bias, bdt, y, ldy, M, N, K, gs);
-  return hipGetLastError();
-}
-
-// ------------------------------------------------------------------------------------------------ dense dequantisation
-// W[n, k] = q[n, k] * s[g(k), n] in fp32, rounded once to bf16 / fp16 (the value the prefill kernel stores into LDS),
-// into a dense [N, ldo] matrix for the dequantise + library GEMM route.  One wavefront per 2048 columns of a row: lane
-// l converts the 16 bytes at columns c0 + 1024 i + 16 l (i = 0, 1) with one nontemporal 16-byte load and two 16-byte
-// stores; the group index is a multiply-high by gmul (group_div_exact holds, else the launcher declines).
-template <bool OBF16>
-__global__ void __launch_bounds__(256) w8_dequant16_kernel(const int8_t* __restrict__ qw, int64_t ldq,
-                                                           const void* __restrict__ scales, int sdt, int64_t lds,
-                                                           uint16_t* __restrict__ out, int64_t ldo, int N, int K,
-                                                           int wpr, uint32_t gdiv, uint32_t gmul) {
-  typedef float f32x2_dq8_t __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2_dq8_t __attribute__((ext_vector_type(2)));
-  typedef _Float16 f16x2_dq8_t __attribute__((ext_vector_type(2)));
-  typedef uint32_t u32x4_dq8_t __attribute__((ext_vector_type(4)));
-  const int64_t wv = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  if (wv >= (int64_t)N * wpr) return;  // whole wavefronts
-  const int lane = threadIdx.x & (kWave - 1);
-  const int n = (int)(wv / wpr), c0 = (int)(wv - (int64_t)n * wpr) * 2048 + 16 * lane;
-  const int8_t* qr = qw + (int64_t)n * ldq;
-  uint16_t* orow = out + (int64_t)n * ldo;
-  u32x4_dq8_t w[2];
-  float sc[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = c0 + 1024 * i;
-    if (c < K) {
-      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_dq8_t*>(qr + c));
-      const uint32_t g = gdiv > 1 ? __umulhi((uint32_t)c, gmul) : (gdiv == 1 ? (uint32_t)c : 0u);
-      sc[i] = load_f(scales, sdt, (int64_t)g * lds + n);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = c0 + 1024 * i;
-    if (c < K) {
-      const uint32_t wd[4] = {w[i][0], w[i][1], w[i][2], w[i][3]};
-      uint32_t h[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t b = wd[j / 2] >> (16 * (j % 2));
-        const f32x2_dq8_t v = {(float)(int8_t)(b & 0xFFu) * sc[i], (float)(int8_t)((b >> 8) & 0xFFu) * sc[i]};
-        if constexpr (OBF16) {
-          h[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_dq8_t));
-        } else {
-          h[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_dq8_t));
-        }
-      }
-      *reinterpret_cast<uint4*>(orow + c) = make_uint4(h[0], h[1], h[2], h[3]);
-      *reinterpret_cast<uint4*>(orow + c + 8) = make_uint4(h[4], h[5], h[6], h[7]);
-    }
-  }
-}
-
-bool w8_dequant16_ok(const int8_t* qw, int64_t ldq, int odt, int64_t K, int gs, int64_t G) {
-  return (odt == FG_BF16 || odt == FG_F16) && K % 16 == 0 && (gs % 16 == 0 || G == 1) && ldq % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(qw) % 16 == 0 && group_div_exact(K, gs, G, 1);
-}
-
-// out[N, ldo] (16-byte aligned rows, ldo % 8 == 0) = q * s rounded to odt; hipErrorInvalidValue outside
-// w8_dequant16_ok.
-hipError_t launch_w8_dequant16(const int8_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds, void* out,
-                               int odt, int64_t ldo, int N, int K, int gs, hipStream_t s) {
-  const int64_t G = (K + gs - 1) / gs;
-  if (!w8_dequant16_ok(qw, ldq, odt, K, gs, G) || ldo % 8 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0)
-    return hipErrorInvalidValue;
-  const int wpr = (K + 2047) / 2048;  // wavefronts per channel row
-  const int64_t blocks = ((int64_t)N * wpr + 3) / 4;
-  const uint32_t gdiv = G == 1 ? 0u : (uint32_t)gs;
-  const uint32_t gmul = gdiv > 1 ? (uint32_t)(0xffffffffu / gdiv + 1u) : 0u;
-  auto kern = odt == FG_BF16 ? w8_dequant16_kernel<true> : w8_dequant16_kernel<false>;
-  note_kernel("w8_dequant16_kernel");
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, s, qw, ldq, scales, sdt, lds,
-                     static_cast<uint16_t*>(out), ldo, N, K, wpr, gdiv, gmul);
   return hipGetLastError();
 }
 

@@ -262,7 +262,8 @@ _W4_IMPLS = {"gemv": "gemv", "dot": "mfma", "mfma": "mfma", "dequant_matmul": "d
 
 def forced_impl() -> str | None:
     """``FORGE_W4_IMPL`` = gemv | mfma | prefill | dequant_gemm | generic (the reference's dot / dequant_matmul / legacy
-    map to mfma / dequant_gemm / generic); anything else means the policy."""
+    map to mfma / dequant_gemm / generic; dequant_gemm names the prefill kernels, which fuse the dequantisation into
+    the MFMA tiles); anything else means the policy."""
     return _W4_IMPLS.get(os.environ.get("FORGE_W4_IMPL", "").strip().lower())
 
 
@@ -430,9 +431,9 @@ def w8a16_linear(x: torch.Tensor, packed: PackedW8, bias: torch.Tensor | None = 
                  config: dict[str, Any] | None = None, deterministic: bool = True) -> torch.Tensor:
     """``y = x @ (q * s)^T (+ bias)`` with symmetric int8 weights (``forge/kernels/ops_gemm.py:320-346``) for bf16 /
     fp16 ``x [..., K]``; returns ``x.dtype``.  A split-K GEMV for 1..4 rows, the LDS-ring and skinny MFMA kernels up
-    to 64 rows, dequantise-to-LDS MFMA tiles beyond, from 768 rows the weights dequantised once into the workspace and
-    hipBLASLt's GEMM, a generic kernel for shapes none of them takes (``config={"impl": "gemv" | "mfma" | "prefill" |
-    "dequant_gemm" | "generic"}`` overrides); fixed-order reductions throughout."""
+    to 64 rows, the dequantise-into-MFMA prefill kernels beyond (the ping-pong kernel on large problems), a generic
+    kernel for shapes none of them takes (``config={"impl": "gemv" | "mfma" | "prefill" | "dequant_gemm" |
+    "generic"}`` overrides; "dequant_gemm" names the prefill kernels); fixed-order reductions throughout."""
     _on_gpu(x, "w8a16_linear")
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise HardwareUnsupported(f"w8a16_linear: activations must be bf16 or fp16, got {x.dtype}")

@@ -35,14 +35,14 @@ enum { FG_OK = 0, FG_EINVAL = 1, FG_EUNSUPPORTED = 2, FG_EHIP = 3 };
 
 /* W4A16 implementation selector (fg_w4_config.impl) */
 enum { FG_W4_AUTO = 0, FG_W4_GEMV = 1, FG_W4_MFMA = 2, FG_W4_GENERIC = 3, FG_W4_PREFILL = 4, FG_W4_DEQUANT_GEMM = 5 };
-/* FG_W4_PREFILL: 128/256 x 256 tiles, x straight to LDS, weights dequantised to LDS (large M x N; needs K % 64 == 0,
-   group % 32 == 0 or one group, aligned x / qweight, no act-order perm)
-   FG_W4_DEQUANT_GEMM: the reference's large-M route (forge/kernels/triton/gemm_w4_dequant.py:194-256): the weights
-   dequantised once into the workspace, then hipBLASLt's bf16 / fp16 GEMM (fp32 accumulation, bias in its epilogue);
-   the policy takes it from 768 rows when the caller's workspace holds it
-   (never in fg_w4a16_gemm_noalloc).  Needs
-   K % 8 == 0, x and y with 16-byte aligned rows (ldx, ldy % 8 == 0), no act-order perm (a g_idx is fine), a bias
-   in fp32 or x's dtype, a 256-byte aligned workspace. */
+/* FG_W4_PREFILL: the prefill kernels, x straight to LDS, weights dequantised tile by tile and fed to bf16 / fp16 MFMA
+   (large M x N; needs K % 64 == 0, group % 32 == 0 or one group, aligned x / qweight, no act-order perm): from 256
+   rows the ping-pong kernel (256 x 256 tiles, two teams of wavefronts alternating MFMA and dequantisation; group %
+   64 == 0, N % 8 == 0, 16-bit scales) once the problem has >= 160 such tiles, else the producer / consumer kernel
+   (256 x 128 tiles), else the all-rounder (128 / 256 x 256 tiles, split-K).  fg_w4_config.tile_n = 256 / 128 / 64
+   forces one of them where its conditions hold.
+   FG_W4_DEQUANT_GEMM: the reference's dequant_matmul route (forge/kernels/triton/gemm_w4_dequant.py:194-256,
+   dequantise then a library GEMM); here a name for FG_W4_PREFILL, whose kernels fuse the two steps. */
 
 /* GEMV kernel selector (fg_w4_config.gemv_kernel) */
 enum { FG_GEMV_AUTO = 0, FG_GEMV_SPLIT = 1, FG_GEMV_TILE = 2, FG_GEMV_WAVE = 3 };
@@ -55,7 +55,8 @@ typedef struct fg_w4_config {
   int32_t tile_m;       /* MFMA: rows of x per workgroup tile (16, 32, 64 or 128); setting it (or split_k) selects
                            the LDS-tiled MFMA kernel over the register-resident split-K kernel used for M <= 64 */
   int32_t split_k;      /* MFMA / PREFILL: K splits (fp32 partials in the workspace, reduced in fixed order) */
-  int32_t tile_n;       /* GEMV tile kernel: output channels per workgroup tile (rounded up to a multiple of 8) */
+  int32_t tile_n;       /* GEMV tile kernel: output channels per workgroup tile (rounded up to a multiple of 8);
+                           PREFILL: 256 / 128 / 64 = ping-pong / producer-consumer / all-round kernel */
   int32_t gemv_kernel;  /* GEMV: FG_GEMV_SPLIT = split-K register kernel (M <= 4, K <= 65536), FG_GEMV_TILE = LDS-tiled
                            kernel, FG_GEMV_WAVE = one-wavefront-per-row-block kernel; AUTO = split when it fits,
                            else tile, else wave.  Setting rows_per_wave implies WAVE, tile_n implies TILE. */
@@ -158,17 +159,12 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
  *   scales   fp16|bf16|fp32 [G, N] (row stride lds);  group_size <= 0: one group per row (per-channel)
  *   cfg      NULL (policy: decode GEMV for 1..2 rows and 3..4 over N <= 8192 and K < 8192; LDS-ring kernel for
  *            17..64 rows and for 3..16 over N >= 16384 or K >= 8192; skinny kernel for the other rows up to 64;
- *            then the prefill kernel; from 768 rows the dequantise + library GEMM route where it applies) or impl
- *            FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny kernel, M <= 64), FG_W4_PREFILL
- *            (dequantise-to-LDS kernel), FG_W4_GENERIC (any shape), FG_W4_DEQUANT_GEMM (q * s rounded once to x's
- *            dtype into the workspace, then hipBLASLt's GEMM with the bias in its epilogue; needs K % 16 == 0,
- *            group % 16 == 0 or one group, ldq % 16 == 0, 16-byte aligned qweight, x and y with 16-byte aligned rows,
- *            a bias in fp32 or x's dtype, a
- *            256-byte aligned workspace and, under graph capture, a first call of the same problem outside it);
- *            split_k for the prefill kernel
- *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernel or, under the policy, of the
- *              LDS-ring kernel, and from 768 rows the route's dequantised weights plus 32 MiB for hipBLASLt; 0 when
- *              none applies)
+ *            then the prefill kernels: from 256 rows the ping-pong kernel once the problem has >= 160 tiles of
+ *            256 x 256, else the all-rounder) or impl FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny
+ *            kernel, M <= 64), FG_W4_PREFILL / FG_W4_DEQUANT_GEMM (the prefill kernels; tile_n = 256 / 64 forces
+ *            the ping-pong / all-round kernel), FG_W4_GENERIC (any shape); split_k for the prefill kernels
+ *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernels or, under the policy, of the
+ *              LDS-ring kernel; 0 when none applies)
  * ------------------------------------------------------------------------------------------------------------- */
 size_t fg_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, const fg_w4_config* cfg);
 int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight, int64_t ldq, const void* scales,

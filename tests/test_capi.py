@@ -67,37 +67,39 @@ def test_mm_config_and_int32_bias_are_validated_before_launch():
 
 
 @pytest.mark.parametrize("m,n,k,expect_ws", [(1, 4096, 4096, False), (4, 4096, 4096, False), (16, 4096, 4096, True),
-                                            (4096, 4096, 4096, True)])
+                                            (512, 4096, 4096, True), (768, 4096, 28672, True), (768, 28672, 4096, False),
+                                            (4096, 4096, 4096, False)])
 def test_workspace_query_follows_the_kernel_plan(m, n, k, expect_ws):
+    """Split-K partials only (no kernel keeps a dequantised copy of the weights): none once the tiles cover the CUs."""
     L = _lib.lib()
     ws = L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, None)
     assert (ws > 0) == expect_ws
-    if ws and m < 768:  # split-K partials
+    if ws:
         assert ws % (m * n * 4) == 0 and ws // (m * n * 4) > 1
-    if m >= 768:  # the dequantise + library GEMM route: the dequantised weights and hipBLASLt's 32 MiB
-        assert ws >= n * k * 2 + (32 << 20)
-        cfg = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
-        assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(cfg)) == n * k * 2 + (32 << 20)
+    # FG_W4_DEQUANT_GEMM (the reference's dequant_matmul) names the prefill kernels: their workspace
+    dq = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
+    pf = _lib.W4Config(_lib.W4_PREFILL, 0, 0, 0, 0)
+    assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(dq)) == \
+        L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(pf))
     # forcing one split removes the workspace
     cfg = _lib.W4Config(_lib.W4_MFMA, 0, 0, 0, 1)
     assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 0, ctypes.byref(cfg)) == 0
-    # the generic kernel never needs one; a g_idx call routes there below 768 rows (from 768 the dequantisation
-    # applies g_idx and the library GEMM follows)
-    gidx_ws = L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 1, None)
-    assert gidx_ws == (0 if m < 768 else n * k * 2 + (32 << 20))
+    # a g_idx call goes to the generic kernel, which never needs one
+    assert L.fg_w4a16_workspace_bytes(m, n, k, 128, 1, 1, 1, None) == 0
 
 
-@pytest.mark.parametrize("m", [768, 4096])
-def test_w8a16_workspace_covers_the_library_route(m):
-    """From 768 rows the W8A16 policy may take the dequantise + library GEMM route: the workspace holds the 16-bit
-    weights and hipBLASLt's 32 MiB; forced, exactly that; a K the dequantisation does not take, none."""
+@pytest.mark.parametrize("m", [512, 768, 4096])
+def test_w8a16_workspace_holds_split_partials_only(m):
+    """The W8A16 prefill kernels' split-K partials (none once the tiles cover the CUs); FG_W4_DEQUANT_GEMM names them."""
     L = _lib.lib()
-    n, k, route = 4096, 4096, 4096 * 4096 * 2 + (32 << 20)
-    assert L.fg_w8a16_workspace_bytes(m, n, k, -1, None) >= route
-    cfg = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
-    assert L.fg_w8a16_workspace_bytes(m, n, k, -1, ctypes.byref(cfg)) == route
-    assert L.fg_w8a16_workspace_bytes(m, n, 4104, -1, ctypes.byref(cfg)) == 0
-    assert L.fg_w8a16_workspace_bytes(4, n, k, -1, ctypes.byref(cfg)) == route
+    n, k = 4096, 4096
+    ws = L.fg_w8a16_workspace_bytes(m, n, k, -1, None)
+    assert ws == 0 or (ws % (m * n * 4) == 0 and ws // (m * n * 4) > 1)
+    assert (ws > 0) == (m < 4096)  # 256 tiles of 256 x 256 at 4096 rows cover the CUs in one pass
+    dq = _lib.W4Config(_lib.W4_DEQUANT_GEMM, 0, 0, 0, 0)
+    pf = _lib.W4Config(_lib.W4_PREFILL, 0, 0, 0, 0)
+    assert L.fg_w8a16_workspace_bytes(m, n, k, -1, ctypes.byref(dq)) == L.fg_w8a16_workspace_bytes(m, n, k, -1,
+                                                                                                    ctypes.byref(pf))
 
 
 def _header_prototypes() -> dict[str, list[str]]:

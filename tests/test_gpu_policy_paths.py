@@ -106,15 +106,17 @@ def test_w4_policy_4_rows_gate_up(xdt):
 
 
 @pytest.mark.parametrize("m,n,k,gs,xdt,sdt", [
-    (2048, 8192, 1024, 128, torch.float16, torch.float16),   # 256 tiles of 256 x 256: the 256-row kernel, fp16 x
+    (2048, 8192, 1024, 128, torch.float16, torch.float16),   # 256 tiles of 256 x 256: the all-rounder's 256-row tiles
     (2048, 8192, 512, -1, torch.bfloat16, torch.float32),    # the same with fp32 scales (plain K loop), one group
 ])
 def test_w4_prefill_256_row_tiles(m, n, k, gs, xdt, sdt):
+    """The all-round prefill kernel (tile_n = 64 forces it; the policy runs the ping-pong kernel on these shapes)."""
     q, s, z = w4_parts(n, k, gs, False, seed=m + k, scale_dtype=sdt)
     p = L.pack_w4(q, s, z, gs).to(DEV)
     x = x_act(m, k, xdt, seed=k)
     b = (torch.randn(n, generator=gen(k)) * 0.5).to(xdt)
-    y = ops.w4a16_linear(x.to(DEV), p, b.to(DEV), config={"impl": "prefill"})
+    y = ops.w4a16_linear(x.to(DEV), p, b.to(DEV), config={"impl": "prefill", "tile_n": 64})
+    assert ops.last_kernel().startswith("w4_big_kernel<256"), ops.last_kernel()
     ref = og.w4a16_gemm_ref(to_f32(x), oracle_packed(q, s, z, gs), to_f32(b))
     assert_close(y.cpu(), ref, ODT[xdt], what=f"prefill 256-row m={m} n={n} k={k}")
 

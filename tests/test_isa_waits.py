@@ -9,7 +9,10 @@ that later loads may stay in flight.  That is only correct while the instruction
 * w4_ring_kernel (W4 on the CDNA4 layout, 33..64 rows or long K): the same rule with NI = 4 MB / BW + T + 2 buffer
   loads into LDS per step;
 * w8a16_ring_kernel (W8A16, 3..64 rows): the same rule with NI = 4 MB / BW + 2 T + 1 (two loads per weight tile, no
-  zero-points).
+  zero-points);
+* w4_pp_kernel (W4A16 / W8A16 ping-pong prefill): every wavefront issues 4 x loads and 3 staging loads per V phase
+  (10 / 14 before its first wait), and waits only with vmcnt(7) (a staging group with an x and a staging group after
+  it) or vmcnt(10) (an x group with three groups after it); between two waits it issues one V phase's 7 loads or none.
 
 A compiler that reorders, splits or adds a load there breaks the check here, on the CPU, instead of silently racing on
 the GPU.  No GPU is used."""
@@ -253,3 +256,80 @@ def test_w8a16_ring_kernel_loop_issues_one_step_and_waits_for_the_next(kernels):
         mb, t, bw, s = (int(v) for v in re.findall(r"Li(\d+)E", name)[:4])
         found += _check_ring_loops(name, code, 4 * mb // bw + 2 * t + 1, s)
     assert found >= 16, f"expected the W8A16 ring instances' loops, checked {found}"
+
+
+def _check_pp(name: str, code: list[tuple[int, str, str]]) -> int:
+    """The ping-pong kernel's load accounting: waits are vmcnt(7) or vmcnt(10); every path from entry issues 10 (team
+    A: stg, x, stg) or 14 (team B: x, stg, x, stg) direct-to-LDS loads before the first wait; every path from a wait to
+    the next issues 0 or 7 and no other vector-memory load.  The kernel branches on the wave-uniform team index with
+    every lane active, so the exec-is-zero skips the compiler leaves around that if / else never fire: their taken
+    edges are not walked.  Returns the waits checked."""
+    addr = {a: i for i, (a, _, _) in enumerate(code)}
+
+    def succ_of(i: int) -> list[int]:
+        nxt = _successors(code, addr, i)
+        return nxt[:1] if code[i][1] == "s_cbranch_execz" else nxt
+    # the kernel's own waits; after the last barrier (the drain) the epilogue's waits for its register loads follow
+    last_barrier = max(i for i, (_, m, _) in enumerate(code) if m == "s_barrier")
+    waits = [(i, n) for i, (_, m, o) in enumerate(code[:last_barrier]) if (n := _vmcnt(m, o))]
+    assert waits and all(n in (7, 10) for _, n in waits), (name, waits)
+    wset = {w for w, _ in waits}
+
+    def walk(starts: list[int]) -> set[tuple[str, int, int]]:
+        ends, seen, todo = set(), set(), [(k, 0, 0) for k in starts]
+        while todo:
+            i, dma, other = todo.pop()
+            if (i, dma, other) in seen:
+                continue
+            seen.add((i, dma, other))
+            assert dma <= 14 and len(seen) < 400000, f"{name}: a path from {starts} issues {dma} DMA loads"
+            if i in wset:
+                ends.add(("wait", dma, other))
+                continue
+            m, o = code[i][1], code[i][2]
+            dma2, other2 = dma + _lds_dma(m, o), min(1, other + (_vmem(m) and not _lds_dma(m, o)))
+            succ = succ_of(i)
+            if not succ:
+                ends.add(("end", dma2, other2))
+            todo.extend((k, dma2, other2) for k in succ)
+        return ends
+
+    first = {d for k, d, _ in walk([0]) if k == "wait"}
+    assert first == {10, 14}, (name, first)
+    for w, _ in waits:
+        for kind, dma, other in walk(succ_of(w)):
+            if kind == "wait":
+                assert dma in (0, 7) and other == 0, f"{name}: {dma} DMA / {other} other loads between waits at {w}"
+            else:
+                assert dma == 0, f"{name}: a path from the wait at {w} to the end issues {dma} DMA loads"
+    return len(waits)
+
+
+def test_pp_kernel_issues_one_v_phase_between_waits(kernels):
+    found = 0
+    for name, code in kernels.items():
+        if "w4_pp_kernel" in name:
+            found += _check_pp(name, code)
+    assert found >= 4 * 4, f"expected the four ping-pong instances' waits, checked {found}"
+
+
+def test_pp_check_rejects_a_planted_extra_load():
+    """The ping-pong walk on a hand-written team-B-like program (14 loads, wait, then a loop of 7 loads and a wait):
+    accepted as written, rejected with an eighth load in the loop, a register load there, or a wait of 8."""
+    def prog(extra: str = "", wait: int = 7, first: int = 10) -> list[tuple[int, str, str]]:
+        dma = ("buffer_load_dwordx4", "v0, s[0:3], 0 offen lds")
+        pro = [dma] * 14 + [("s_waitcnt", f"vmcnt({wait})"), ("s_barrier", "")]
+        loop = [dma] * 7 + ([("buffer_load_dword", extra)] if extra else []) + \
+            [("s_barrier", ""), ("s_waitcnt", f"vmcnt({wait})"), ("s_barrier", ""), ("s_cbranch_scc1", "<k+0x{:x}>")]
+        team_a = [dma] * first + [("s_waitcnt", "vmcnt(7)"), ("s_barrier", "")]
+        code = [("s_cbranch_scc0", "<k+0x{:x}>")] + pro + loop + [("s_branch", "<k+0x{:x}>")] + team_a + \
+            [("s_waitcnt", "vmcnt(0)"), ("s_barrier", ""), ("s_endpgm", "")]
+        loop0, a0 = 1 + len(pro), 1 + len(pro) + len(loop) + 1
+        end = a0 + len(team_a)
+        targets = {0: a0, loop0 + len(loop) - 1: loop0, a0 - 1: end}
+        return [(0x1000 + 4 * i, m, o.format(4 * targets[i]) if i in targets else o) for i, (m, o) in enumerate(code)]
+
+    assert _check_pp("ok", prog()) == 3
+    for bad in (prog("v0, s[0:3], 0 offen lds"), prog("v2, s[0:3], 0 offen"), prog(wait=8), prog(first=11)):
+        with pytest.raises(AssertionError):
+            _check_pp("bad", bad)
