@@ -24,9 +24,10 @@ same operands (``vendor``).  Every timed row reports the mean with the median an
 to the process) on configs[0], plus one FP8 and one INT8 GEMM at M=4096.
 
 Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1]``; prints one JSON line.
-``python bench.py --pmc-workload [gemv|decode|w8a8]``: only a 256 MiB device copy (counter calibration) and the named
-kernels, eager, for ``rocprofv3 --pmc`` passes (gemv: 64 gate+up GEMV launches; decode: the CDNA4-layout kernel at
-M=16/64 on the four shapes; w8a8: the FP8 / INT8 GEMMs at M=4096).
+``python bench.py --pmc-workload [gemv|decode|w8a8|prefill]``: only a 256 MiB device copy (counter calibration) and the
+named kernels, eager, for ``rocprofv3 --pmc`` passes (gemv: 64 gate+up GEMV launches; decode: the CDNA4-layout kernel
+at M=16/64 on the four shapes; w8a8: the FP8 / INT8 GEMMs at M=4096; prefill: the ping-pong prefill kernel at
+M=8192).
 """
 from __future__ import annotations
 
@@ -356,7 +357,9 @@ def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
     gemv   -- the gate+up GEMV (K=4096, N=28672, M=1) over a ring of 32 weights, twice (64 launches);
     decode -- the CDNA4-layout W4 kernel at M=16 and M=64 on the four Llama-3-8B shapes, over a ring of 6 weights per
               shape, twice (12 launches per shape and M);
-    w8a8   -- the FP8 GEMM at M=4096, K=N=8192 and the INT8 GEMM at M=4096, K=8192, N=10240, 5 launches each."""
+    w8a8   -- the FP8 GEMM at M=4096, K=N=8192 and the INT8 GEMM at M=4096, K=8192, N=10240, 5 launches each;
+    prefill -- the W4A16 ping-pong prefill kernel at M=8192 on gate+up and down and the W8A16 one on gate+up, 5
+              launches each."""
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -386,6 +389,26 @@ def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
                 torch.cuda.synchronize()
             del ring
         log("pmc workload done: 3 x 256 MiB copy, CDNA4-layout W4 at M=16/64 x 4 shapes x 12 launches")
+    elif which == "prefill":
+        m = 8192
+        for name, bits in (("gate_up", 4), ("down", 4), ("gate_up", 8)):
+            k, n = SHAPES[name]
+            x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+            if bits == 4:
+                p = make_layer_weights(torch, layouts, dev, k, n, gen)
+                fn = ops.w4a16_linear
+            else:
+                p = layouts.PackedW8(torch.randint(-128, 128, (n, k), dtype=torch.int8, device=dev, generator=gen),
+                                     (torch.rand(1, n, device=dev, generator=gen) * 0.018 + 0.002).half(),
+                                     layouts.PORTABLE_W8, n, k, -1)
+                fn = ops.w8a16_linear
+            torch.cuda.synchronize()
+            for _ in range(5):
+                fn(x, p)
+            torch.cuda.synchronize()
+            log(f"pmc prefill {name} W{bits}: {ops.last_kernel()}")
+            del x, p
+        log("pmc workload done: 3 x 256 MiB copy, prefill M=8192 W4 gate_up / down, W8 gate_up x 5 launches")
     elif which == "w8a8":
         m = 4096
         x = torch.randn(m, 8192, device=dev, generator=gen).bfloat16()
@@ -498,7 +521,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the W4A16 M=4..64 decode and prefill sweeps")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
-    ap.add_argument("--pmc-workload", nargs="?", const="gemv", default=None, choices=("gemv", "decode", "w8a8"),
+    ap.add_argument("--pmc-workload", nargs="?", const="gemv", default=None,
+                    choices=("gemv", "decode", "w8a8", "prefill"),
                     help="run only a counter-pass workload (no timing): gemv (default), decode or w8a8")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -29,7 +29,9 @@
 // `s_waitcnt vmcnt(N)` with a constant N means exactly "these loads have landed" (loads complete in issue order; the
 // loads are invisible to the compiler's wait analysis, so every wait is explicit; the ISA test checks the counts).
 //
-// LDS per stage: x 256 rows x 128 B (16-byte unit c of row r at c ^ (r & 7): conflict-free fragment reads) and eight
+// LDS per stage: x 256 rows x 128 B (16-byte unit c of row r at c ^ key(r), key(r) = (r & 7) ^ ((r >> 3) & 1): for
+// fragment reads of units 2 (lane / 16) + k this is free of bank conflicts on gfx950 (SQ_LDS_BANK_CONFLICT), where
+// r & 7 alone costs 4 cycles per read, as in fg_mm_big.hip's FP8 reads) and eight
 // staging areas (packed weights of 32 channels: 32 B (W8A16: 64 B) per channel, scales 256 B, zero words 256 B).  Three
 // stages: 135168 bytes (W8A16 153600).
 //
@@ -197,15 +199,17 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   const u32x4_t rx = pp_rsrc(a.x, a.xbytes), rq = pp_rsrc(a.qw, a.qbytes);
   const u32x4_t rs = pp_rsrc(a.scales, a.sbytes), rz = pp_rsrc(a.zeros, a.zbytes);
   // x: load i of wavefront w fills tile rows 8 xg + 8 i .. + 8 with xg = 8 wq + 4 (1 - team) (team B the first half of
-  // rows 64 wq .. + 64, team A the second); lane l writes position l % 8 of row 8 xg + 8 i + l / 8, i.e. global unit
-  // (l % 8) ^ (l / 8) (the row's swizzle key is l / 8)
+  // rows 64 wq .. + 64, team A the second); lane l writes position l % 8 of row r = 8 (xg + i) + l / 8, i.e. global
+  // unit (l % 8) ^ key(r) with key(r) = (l / 8) ^ ((xg + i) & 1)
   const int xg = 8 * wq + 4 * (1 - team);
   uint32_t xv[kPpXI];
   {
-    const int lrow = lane >> 3, lunit = (lane & 7) ^ (lane >> 3);
+    const int lrow = lane >> 3;
 #pragma unroll
-    for (int i = 0; i < kPpXI; ++i)
+    for (int i = 0; i < kPpXI; ++i) {
+      const int lunit = (lane & 7) ^ (lane >> 3) ^ ((xg + i) & 1);
       xv[i] = (uint32_t)min(m0 + (xg + i) * 8 + lrow, a.M - 1) * (uint32_t)a.ldx * 2u + 16u * (uint32_t)lunit;
+    }
   }
   // packed weights: load h fills 1 KiB of the wavefront's staging: W4 channels l / 2 (16-byte half l % 2 of a 32-byte
   // slice row), W8 channels 16 h + l / 4 (quarter l % 4 of a 64-byte row)
@@ -305,9 +309,10 @@ __global__ void __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu
   // MFMAs, read kPpAhead ahead
   auto mphase = [&](int s) __attribute__((always_inline)) {
     const uint8_t* arow = stage(s) + r16 * kPpRow;
+    const int rkey = (r16 & 7) ^ (r16 >> 3);  // key of rows 16 i + r16
     auto read_a = [&](int g) __attribute__((always_inline)) {
       const int k = g >> 4, i = g & 15;
-      return *reinterpret_cast<const uint4*>(arow + i * 16 * kPpRow + (((2 * j4 + k) ^ (r16 & 7)) * 16));
+      return *reinterpret_cast<const uint4*>(arow + i * 16 * kPpRow + (((2 * j4 + k) ^ rkey) * 16));
     };
     uint4 f[kPpAhead];
 #pragma unroll
