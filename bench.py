@@ -127,48 +127,38 @@ def time_eager(torch, fn, reps: int, warmup: int) -> Timing:
 
 def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -> tuple[dict, dict]:
     """configs[1] decode sweep at M in {4, 16, 64} (GB/s of algorithmic bytes, HIP-graph replays over the 32-layer
-    ring) and configs[2] prefill at M in {512, 2048, 8192} (TFLOP/s against bf16 dense MFMA, one weight per shape)."""
+    ring) and configs[2] prefill at M in {512, 2048, 8192} (TFLOP/s against bf16 dense MFMA, one weight per shape).
+    The decode rows ``M4 / M16 / M64`` go through KernelW4A16Linear, the module a served model runs (portable_row
+    weights plus the CDNA4-layout copy its prepare() keeps for 3..64 rows); ``M*_portable_row`` are the raw op on the
+    portable_row weights alone."""
     decode = {}
+
+    def sweep(label: str, m: int, weights: list, call) -> None:
+        row = {}
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
+        for name, (k, n) in SHAPES.items():
+            sel = [(xs[k], w) for nm, w in weights if nm == name]
+
+            def run(sel=sel):
+                for x, w in sel:
+                    call(x, w)
+
+            t = timer(torch, run, steps, warmup) / len(sel)
+            gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
+            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "kernel": ops.last_kernel()}
+        decode[label] = row
+        log(f"decode {label}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
+
+    portable = [(nm, p) for nm, _, p in ring]
     for m in (4, 16, 64):
-        row = {}
-        xs = {k: torch.randn(m, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
-        for name, (k, n) in SHAPES.items():
-            sel = [(xs[k], p) for nm, _, p in ring if nm == name]
-
-            def run(sel=sel):
-                for x, p in sel:
-                    ops.w4a16_linear(x, p)
-
-            t = timer(torch, run, steps, warmup) / len(sel)
-            gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
-            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "kernel": ops.last_kernel()}
-        decode[f"M{m}"] = row
-        log(f"decode M={m}: " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for nm, v in row.items()))
-    # the same weights repacked at load time into the CDNA4 MFMA-fragment layout (a bit-exact permutation), read by
-    # its own kernel at 16 and 64 rows
-    from forge_amd import layouts
-
-    frag = [(nm, layouts.repack(p, layouts.CDNA4_W4)) for nm, _, p in ring]
+        sweep(f"M{m}_portable_row", m, portable, lambda x, p: ops.w4a16_linear(x, p))
+    # the modules a model loader swaps in: the same portable_row tensors, and the CDNA4-layout copy each keeps
+    mods = [(nm, ops.KernelW4A16Linear.from_packed(p)) for nm, p in portable]
     torch.cuda.synchronize()
-    for m in (16, 64):
-        row = {}
-        xs = {k: torch.randn(m, k, device=dev, generator=gen).bfloat16() for k in {k for k, _ in SHAPES.values()}}
-        for name, (k, n) in SHAPES.items():
-            sel = [(xs[k], p) for nm, p in frag if nm == name]
-
-            def run(sel=sel):
-                for x, p in sel:
-                    ops.w4a16_linear(x, p)
-
-            t = timer(torch, run, steps, warmup) / len(sel)
-            gbs = w4_bytes(m, k, n) / (t * 1e-3) / 1e9
-            row[name] = {"us": round(t * 1e3, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "kernel": ops.last_kernel()}
-        decode[f"M{m}_cdna4_layout"] = row
-        log(f"decode M={m} (cdna4 layout): " + "  ".join(f"{nm} {v['us']:.2f} us {v['GBps']:.0f} GB/s"
-                                                       for nm, v in row.items()))
-    del frag
+    for m in (4, 16, 64):
+        sweep(f"M{m}", m, mods, lambda x, mod: mod(x))
+    del mods
     prefill = {}
     dense = {name: torch.randn(n, k, device=dev, generator=gen).bfloat16() for name, (k, n) in SHAPES.items()}
     for m in (512, 2048, 8192):

@@ -31,6 +31,7 @@ import torch.nn as nn
 from . import _lib
 from .errors import ConfigError, HardwareUnsupported, KernelCorrectnessError
 from .layouts import (
+    CDNA4_W4,
     KIND_CDNA4,
     KIND_PORTABLE,
     MISSING_SORT,
@@ -362,6 +363,22 @@ def _cdna4_fits(p: PackedW4, m: int, config: dict[str, Any] | None) -> bool:
             and impl in (None, "mfma"))
 
 
+# Rows for which a portable_row weight's CDNA4-layout copy (kept by KernelW4A16Linear.prepare) serves the call: its MFMA
+# kernels beat the portable_row policy there (graph replays, us, portable / CDNA4: M = 16 qkv 10.2 / 8.8, o_proj 8.2 /
+# 7.5, gate+up 22.1 / 18.0, down 15.8 / 14.4; M = 64 17.6 / 16.7, 14.4 / 13.8, 35.9 / 32.5, 25.2 / 23.6); one or two
+# rows stay on the split-K GEMV.
+CDNA4_COPY_ROWS = (3, 64)
+
+
+def _cdna4_copy(packed: PackedW4) -> PackedW4 | None:
+    """The CDNA4-layout copy kept beside a portable_row weight, if one was made and its tensors have not changed."""
+    copies = packed.meta.get("hip.layout_copies") if packed.meta is not None else None
+    hit = copies.get(CDNA4_W4.id) if copies else None
+    if hit is None:
+        return None
+    return hit[1] if hit[0] == tuple((t.data_ptr(), t._version) for t in packed.tensors().values()) else None
+
+
 def _w4_cdna4_call(x2: torch.Tensor, p: PackedW4, bias: torch.Tensor | None, y: torch.Tensor) -> None:
     m, k = x2.shape
     z = p.zeros
@@ -399,7 +416,11 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
     y = torch.empty((m, packed.n), dtype=x.dtype, device=x.device)
     if m:
         b = None if bias is None else bias.contiguous()
-        if _cdna4_fits(packed, m, config):
+        copy = (_cdna4_copy(packed) if packed.layout.kind == KIND_PORTABLE
+                and CDNA4_COPY_ROWS[0] <= m <= CDNA4_COPY_ROWS[1] else None)
+        if copy is not None and _cdna4_fits(copy, m, config):
+            _w4_cdna4_call(x2, copy, b, y)
+        elif _cdna4_fits(packed, m, config):
             _w4_cdna4_call(x2, packed, b, y)
         else:
             if packed.layout.kind == KIND_CDNA4:
@@ -856,13 +877,25 @@ class KernelW4A16Linear(_PackedLinear):
 
     def prepare(self) -> KernelW4A16Linear:
         """Host-synchronising preparation (repack, act-order sort) done now, so forward never syncs; runs after
-        ``load_state_dict`` and ``.to()``.  A weight still all zeros (not loaded yet) is skipped."""
+        ``load_state_dict`` and ``.to()``.  On the GPU a portable_row weight also gets a CDNA4-layout copy for 3..64-row
+        calls (``CDNA4_COPY_ROWS``; the state dict stays portable_row; ``FORGE_W4_CDNA4_COPY=0`` turns it off)."""
         if self.g_idx is not None or self.layout.kind != KIND_PORTABLE:
             try:
                 prepare_w4(self.packed())
             except (ConfigError, RuntimeError) as e:  # forward prepares lazily outside capture
                 log.debug("W4 prepare deferred: %s", e)
+        elif self._cdna4_copy_wanted():
+            try:
+                prepare_w4(self.packed(), CDNA4_W4)
+            except (ConfigError, RuntimeError) as e:
+                log.debug("W4 CDNA4 copy not made: %s", e)
         return self
+
+    def _cdna4_copy_wanted(self) -> bool:
+        """A portable_row weight on the GPU in a shape the CDNA4-layout kernels take."""
+        return (os.environ.get("FORGE_W4_CDNA4_COPY", "1") != "0" and self.qweight.is_cuda and self.g_idx is None
+                and self.in_features % 128 == 0 and (self.group_size <= 0 or self.group_size % 128 == 0)
+                and self.scales.dtype in (torch.float16, torch.bfloat16))
 
     def _apply(self, fn: Callable, *args: Any, **kwargs: Any) -> KernelW4A16Linear:
         out = super()._apply(fn, *args, **kwargs)

@@ -135,3 +135,30 @@ def test_w8a8_module_quantised_on_host_then_moved(kind, kw):
     fresh = ops.make_packed_linear(kind, in_features=k, out_features=n, bias=torch.zeros(n), device=DEV, **kw)
     fresh.load_state_dict(host.state_dict())
     assert torch.equal(fresh(x), y)
+
+
+@pytest.mark.parametrize("m", [1, 16, 64])
+def test_w4a16_module_keeps_a_cdna4_copy_for_decode_rows(m, monkeypatch):
+    """A portable_row module on the GPU keeps a CDNA4-layout copy and serves 3..64-row calls from it (one row stays on
+    the split-K GEMV); its state dict stays portable_row; the copy follows a state-dict load; FORGE_W4_CDNA4_COPY=0
+    keeps every call on portable_row.  Each path against the oracle."""
+    n, k, gs = 1536, 2048, 128
+    q, s, z = w4_parts(n, k, gs, False, seed=m + 40)
+    mod = ops.KernelW4A16Linear.from_packed(L.pack_w4(q, s, z, gs).to(DEV))
+    x = x_act(m, k, torch.bfloat16, seed=m + 41).to(DEV)
+    ref = og.w4a16_gemm_ref(to_f32(x.cpu()), oracle_packed(q, s, z, gs))
+    y = mod(x)
+    kern = ops.last_kernel()
+    assert ("cdna4" in kern or "w4_frag_kernel" in kern) == (m > 1), kern
+    assert_close(y.cpu(), ref, "bfloat16", what=f"module with CDNA4 copy m={m}")
+    sd = mod.state_dict()
+    assert sd["qweight"].shape == L.pack_w4(q, s, z, gs).qweight.shape  # portable_row in the checkpoint
+    fresh = ops.make_packed_linear("w4a16", in_features=k, out_features=n, group_size=gs, sym=False,
+                                   dtype=torch.float16, device=DEV)
+    fresh.load_state_dict(sd)
+    assert torch.equal(fresh(x), y), "the reloaded module's copy does not match"
+    monkeypatch.setenv("FORGE_W4_CDNA4_COPY", "0")
+    plain = ops.KernelW4A16Linear.from_packed(L.pack_w4(q, s, z, gs).to(DEV))
+    yp = plain(x)
+    assert "w4_frag_kernel" not in ops.last_kernel() and "cdna4" not in ops.last_kernel()
+    assert_close(yp.cpu(), ref, "bfloat16", what=f"module without copy m={m}")
