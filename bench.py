@@ -191,7 +191,7 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
 def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -> dict:
     """W8A16 (int8 weight-only, per-channel fp16 scales) decode on the four Llama-3-8B shapes at M in {1, 16, 64}: HBM
     GB/s of algorithmic bytes (N*K weights + 2*N scales + 2*M*K + 2*M*N), HIP-graph replays over a ring of distinct
-    weights (at least 1.2 GB per shape)."""
+    weights (at least 1.2 GB per shape); prefill at M in {2048, 8192}: TFLOP/s, replays over four of those weights."""
     out = {}
     for name, (k, n) in SHAPES.items():
         nring = max(4, (1200 << 20) // (n * k) + 1)
@@ -210,8 +210,21 @@ def bench_w8a16(torch, layouts, ops, dev, gen, timer, steps: int, warmup: int) -
             by = n * k + 2 * n + 2 * m * (k + n)
             row[f"M{m}"] = {"us": round(t * 1e3, 3), "GBps": round(by / (t * 1e-3) / 1e9, 1),
                             "frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": ops.last_kernel()}
-        out[name] = row
         log(f"w8a16 {name:8s}: " + "  ".join(f"M={mm[1:]} {v['us']:.2f} us {v['GBps']:.0f} GB/s" for mm, v in row.items()))
+        for m in (2048, 8192):  # prefill: the ping-pong / 64-channel kernels, TFLOP/s against bf16 dense MFMA
+            x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+
+            def run(x=x, ws=ring[:4]):
+                for p in ws:
+                    ops.w8a16_linear(x, p)
+
+            t = time_graph(torch, run, max(5, steps // 2), 2) / 4
+            tf = 2.0 * m * n * k / (t * 1e-3) / 1e12
+            row[f"M{m}"] = {"ms": round(t, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                            "kernel": ops.last_kernel()}
+            log(f"w8a16 {name:8s}: M={m} {t:.3f} ms {tf:.0f} TF  {ops.last_kernel()}")
+            del x
+        out[name] = row
         del ring
     return out
 

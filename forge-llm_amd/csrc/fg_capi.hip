@@ -315,14 +315,29 @@ int prefill_kernel(int tile_n, int64_t M, int64_t N, bool pp, bool pc, bool big,
   return big ? 2 : 0;
 }
 
-// Split-K workspace of the prefill kernel prefill_kernel picks for this shape and tile_n, and of those it falls back to
-// when the operands rule a kernel out at launch (the ping-pong kernel falls back to the producer / consumer kernel,
-// W4 only, and both to the all-rounder).
+// W8A16 has no producer / consumer kernel.  Below kPpMinTiles tiles from 256 rows, the ping-pong kernel with its K
+// split two or four ways (the fewest that bring tiles x splits to kPpMinTiles) still beats the all-rounder; where four
+// ways stay short of it, the all-rounder wins (graph replays over four distinct weights, us, all-rounder / ping-pong
+// split 2 / split 4: qkv M = 512 65.7 / 66.3 / 51.2, M = 1024 86.9 / 77.8 / 90.9; o_proj M = 512 44.8 / 62.8 / 46.0,
+// M = 1024 67.1 / 70.4 / 61.3, M = 2048 96.4 / 93.8 / 114.2; down M = 512 95.4 / 163.8 / 98.9, M = 1024 159.0 /
+// 174.9 / 133.7, M = 2048 262.8 / 228.5 / 243.6).  Returns that split, 1 from kPpMinTiles tiles, 0 for the
+// all-rounder.
+int w8_pp_split(int64_t M, int64_t N) {
+  if (M < 256) return 0;
+  const int64_t t = pp_tiles(M, N);
+  return t >= kPpMinTiles ? 1 : (2 * t >= kPpMinTiles ? 2 : (4 * t >= kPpMinTiles ? 4 : 0));
+}
+
+// Split-K workspace of the prefill kernel prefill_kernel picks for this shape and tile_n (for W8A16 also the split
+// ping-pong launch w8_pp_split picks), and of those it falls back to when the operands rule a kernel out at launch
+// (the ping-pong kernel falls back to the producer / consumer kernel, W4 only, and both to the all-rounder).
 size_t prefill_workspace_bytes(int tile_n, int64_t M, int64_t N, int64_t K, int split_k, bool w4) {
   const bool pp = tile_n == 256 || (tile_n == 0 && M >= 256 && pp_tiles(M, N) >= kPpMinTiles);
   const bool pc = w4 && (tile_n == 128 || tile_n == 256 || (tile_n == 0 && M >= 256));
   size_t b = fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, split_k, !w4);
   if (pp) b = std::max(b, fg::w4_pp_workspace_bytes((int)M, (int)N, (int)K, split_k));
+  if (!w4 && tile_n == 0 && w8_pp_split(M, N) > 1)
+    b = std::max(b, fg::w4_pp_workspace_bytes((int)M, (int)N, (int)K, split_k > 0 ? split_k : w8_pp_split(M, N)));
   if (pc) b = std::max(b, fg::w4_pc_workspace_bytes((int)M, (int)N, (int)K, split_k));
   return b;
 }
@@ -745,11 +760,17 @@ int fg_w8a16_gemm(const void* x, int64_t ldx, int x_dtype, const int8_t* qweight
     e = fg::launch_w8a16_skinny(x, ldx, xbf16, qweight, ldq, scales, scale_dtype, lds, bias, bias_dtype, y, ldy,
                                 (int)M, (int)N, (int)K, gs, G == 1, s);
   } else if (kern == 2) {
-    // the ping-pong kernel or the all-rounder, by the W4A16 rule (no producer / consumer kernel for int8 weights)
+    // the ping-pong kernel or the all-rounder, by the W4A16 rule; where W4A16 would take the producer / consumer
+    // kernel (none for int8 weights), the ping-pong kernel with its K split as w8_pp_split says
     const bool pp = fg::w8_pp_ok(x, ldx, qweight, ldq, scales, scale_dtype, lds, M, N, K, gs, G) &&
                     !(cfg && cfg->tile_m);
-    const int pk = prefill_kernel(cfg ? cfg->tile_n : 0, M, N, pp, false, big, false);
-    const int split = cfg ? cfg->split_k : 0;
+    const int tn = cfg ? cfg->tile_n : 0;
+    int pk = prefill_kernel(tn, M, N, pp, false, big, false);
+    int split = cfg ? cfg->split_k : 0;
+    if (pk != 5 && pp && tn == 0 && w8_pp_split(M, N) > 1) {
+      pk = 5;
+      if (split <= 0) split = w8_pp_split(M, N);
+    }
     const size_t need = pk == 5 ? fg::w4_pp_workspace_bytes((int)M, (int)N, (int)K, split)
                                 : fg::w4_big_workspace_bytes((int)M, (int)N, (int)K, split, true);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))

@@ -1,7 +1,8 @@
 """GPU parity of the W8A16 prefill kernels (the reference's w8a16_linear at large M, forge/kernels/ops_gemm.py:320-346
 -> gemm_wq.py:138-205 with bits=8): the ping-pong kernel's int8 form (256 x 256 tiles, fg_w4_pp.hip) and the
 all-rounder's (fg_w4_big.hip).  Cases: the policy's choice from 256 rows (ping-pong once a problem has >= 160 tiles of
-256 x 256, else the all-rounder) on Llama-3-8B shapes; each kernel forced (tile_n = 256 / 64) on ragged shapes (one
+256 x 256; below that ping-pong with K split 2 or 4 ways when that reaches 160 tiles x splits, else the all-rounder) on
+Llama-3-8B shapes; each kernel forced (tile_n = 256 / 64) on ragged shapes (one
 row, M and N not multiples of the tile, bias in x's dtype / fp32 / none, per-channel and grouped fp16 / bf16 scales,
 fp16 and bf16 x) and with forced K splits; "dequant_gemm" giving the same bits as "prefill"; fp32 scales and unaligned
 x leaving the ping-pong kernel; graph replays; run-to-run reproducibility.
@@ -41,11 +42,13 @@ def _run(m, n, k, gs, xdt, bdt, *, seed, sdt=torch.float16, config=None):
 
 
 @pytest.mark.parametrize("m,k,n,gs,xdt,bdt,expect", [
-    (768, 4096, 28672, -1, torch.bfloat16, torch.bfloat16, "w4_pp_kernel"),   # 336 tiles
-    (4096, 4096, 4096, 128, torch.float16, torch.float32, "w4_pp_kernel"),    # 256 tiles
-    (1024, 4096, 6144, -1, torch.bfloat16, torch.bfloat16, "w4_big_kernel"),  # 96 tiles
-    (1024, 14336, 4096, -1, torch.bfloat16, None, "w4_big_kernel"),
-    (2048, 4096, 2048, 64, torch.float16, torch.float16, "w4_big_kernel"),
+    (768, 4096, 28672, -1, torch.bfloat16, torch.bfloat16, "w4_pp_kernel<bf16,w8> 256x256 splits=1"),  # 336 tiles
+    (4096, 4096, 4096, 128, torch.float16, torch.float32, "w4_pp_kernel<f16,w8> 256x256 splits=1"),    # 256 tiles
+    (1024, 4096, 6144, -1, torch.bfloat16, torch.bfloat16, "w4_pp_kernel<bf16,w8> 256x256 splits=2"),  # 96 tiles
+    (1024, 14336, 4096, -1, torch.bfloat16, None, "w4_pp_kernel<bf16,w8> 256x256 splits=4"),           # 64 tiles
+    (2048, 4096, 2048, 64, torch.float16, torch.float16, "w4_pp_kernel<f16,w8> 256x256 splits=4"),     # 64 tiles
+    (512, 4096, 4096, -1, torch.bfloat16, torch.bfloat16, "w4_big_kernel"),                            # 32 tiles
+    (300, 14336, 4096, 128, torch.float16, None, "w4_big_kernel"),                                     # 32 tiles
 ])
 def test_policy_choice_from_256_rows(m, k, n, gs, xdt, bdt, expect):
     y, ref, kern, (x, p, bd) = _run(m, n, k, gs, xdt, bdt, seed=m + n)
