@@ -38,13 +38,12 @@ __device__ __forceinline__ f32x4_fr_t fr_mfma(uint4 a, uint4 b, f32x4_fr_t c) {
   }
 }
 
-// (a & mask) | magic in one VOP3 (mask in a scalar register, magic in a vector register: the encoding takes no
-// literal, and left to itself the compiler emits a v_and + v_or pair with literals)
-__device__ __forceinline__ uint32_t fr_and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
-  return r;
-}
+// (a & mask) | magic: one v_and_or_b32 once the caller has hidden the constants from the compiler (mask in a scalar
+// register, magic in a vector register; with literals it emits a v_and + v_or pair).  Plain C rather than inline asm:
+// the result feeds MFMA B operands, and the hazard recognizer inserts the wait states a VALU write needs before an
+// MFMA reads it only for instructions it can see (an asm v_and_or_b32 one instruction ahead of its MFMA produced
+// wrong products).
+__device__ __forceinline__ uint32_t fr_and_or(uint32_t a, uint32_t mask, uint32_t magic) { return (a & mask) | magic; }
 
 // one k-step's word -> the lane's eight B values (columns 8 j .. 8 j + 7 of the k-step) as four exact 16-bit pairs
 __device__ __forceinline__ uint4 fr_unpack(uint32_t w, uint32_t mask, uint32_t magic) {
@@ -136,8 +135,9 @@ __global__ void __launch_bounds__(w4_frag_max_threads(MB, T)) w4_frag_kernel(
     for (int i = 0; i < MB; ++i) acc[t][i] = f32x4_fr_t{0.f, 0.f, 0.f, 0.f};
 
   const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
-  const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-  const uint32_t magic = XBF16 ? 0x43004300u : 0x64006400u;
+  uint32_t mask = 0x000F000Fu, magic = XBF16 ? 0x43004300u : 0x64006400u;
+  asm("" : "+s"(mask));  // opaque to constant folding: v_and_or_b32 with a scalar mask and a vector magic
+  asm("" : "+v"(magic));
   auto compute = [&](const Buf& b) __attribute__((always_inline)) {
     uint4 bw[T][4];
     float sc[T], zb[T];

@@ -50,13 +50,12 @@ __device__ __forceinline__ f32x4_rg_t rg_mfma(uint4 a, uint4 b, f32x4_rg_t c) {
   }
 }
 
-// (a & mask) | magic in one VOP3 (mask in a scalar register, magic in a vector register: the encoding takes no
-// literal, and left to itself the compiler emits a v_and + v_or pair with literals)
-__device__ __forceinline__ uint32_t rg_and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
-  return r;
-}
+// (a & mask) | magic: one v_and_or_b32 once the caller has hidden the constants from the compiler (mask in a scalar
+// register, magic in a vector register; with literals it emits a v_and + v_or pair).  Plain C rather than inline asm:
+// the result feeds MFMA B operands, and the hazard recognizer inserts the wait states a VALU write needs before an
+// MFMA reads it only for instructions it can see (an asm v_and_or_b32 one instruction ahead of its MFMA produced
+// wrong products).
+__device__ __forceinline__ uint32_t rg_and_or(uint32_t a, uint32_t mask, uint32_t magic) { return (a & mask) | magic; }
 
 // one k-step's word -> the lane's eight B values as four exact 16-bit pairs
 __device__ __forceinline__ uint4 rg_unpack(uint32_t w, uint32_t mask, uint32_t magic) {
@@ -216,8 +215,9 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   for (int t = 0; t < T; ++t)
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[t][i] = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
-  const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-  const uint32_t magic = XBF16 ? 0x43004300u : 0x64006400u;
+  uint32_t mask = 0x000F000Fu, magic = XBF16 ? 0x43004300u : 0x64006400u;
+  asm("" : "+s"(mask));  // opaque to constant folding: v_and_or_b32 with a scalar mask and a vector magic
+  asm("" : "+v"(magic));
   const uint4 ones = make_uint4(kOnes, kOnes, kOnes, kOnes);
 
   // row sums by step parity: step i's are written into xsb[i % 2] and read at step i + 1

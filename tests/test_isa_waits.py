@@ -333,3 +333,68 @@ def test_pp_check_rejects_a_planted_extra_load():
     for bad in (prog("v0, s[0:3], 0 offen lds"), prog("v2, s[0:3], 0 offen"), prog(wait=8), prog(first=11)):
         with pytest.raises(AssertionError):
             _check_pp("bad", bad)
+
+
+VREG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
+MFMA_AB_WAIT = 2  # wait states between a VALU write of a VGPR and an MFMA reading it as SrcA / SrcB
+
+
+def _vgprs(text: str) -> set[int]:
+    out: set[int] = set()
+    for m in VREG.finditer(text):
+        if m.group(3):
+            out.add(int(m.group(3)))
+        else:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return out
+
+
+def _valu_to_mfma_gaps(code: list[tuple[int, str, str]]) -> list[tuple[int, int]]:
+    """(index, wait states) of every VALU instruction whose VGPR result a following MFMA of the same straight-line run
+    reads as SrcA or SrcB, with fewer than MFMA_AB_WAIT wait states between them (each instruction between counts one,
+    s_nop N counts N + 1).  The compiler keeps that distance for the code it can see; inline assembly is opaque to its
+    hazard recognizer, so a VALU op written in asm can land closer and the MFMA then reads a stale operand."""
+    bad = []
+    for i, (_, mnem, ops) in enumerate(code):
+        if not mnem.startswith("v_") or mnem.startswith(("v_mfma", "v_cmp", "v_readfirstlane", "v_readlane")):
+            continue
+        dst = _vgprs(ops.split("//")[0].split(",")[0])
+        if not dst:
+            continue
+        waits = 0
+        for _, m2, o2 in code[i + 1:i + 1 + MFMA_AB_WAIT + 1]:
+            if m2.startswith(("s_branch", "s_cbranch", "s_endpgm", "s_setpc")):
+                break
+            if m2.startswith("v_mfma"):
+                srcs = o2.split("//")[0].split(",")
+                if len(srcs) >= 3 and dst & (_vgprs(srcs[1]) | _vgprs(srcs[2])) and waits < MFMA_AB_WAIT:
+                    bad.append((i, waits))
+                break
+            waits += int(o2.split()[0]) + 1 if m2 == "s_nop" and o2.split() else 1
+            if waits >= MFMA_AB_WAIT:
+                break
+    return bad
+
+
+def test_no_valu_result_reaches_an_mfma_operand_too_early(kernels):
+    """Every kernel of the library (the ring and register-ring kernels once built their nibble unpack from an asm
+    v_and_or_b32 that the scheduler placed one instruction ahead of the MFMA reading it: wrong products)."""
+    checked = 0
+    for name, code in kernels.items():
+        assert not _valu_to_mfma_gaps(code), (name, _valu_to_mfma_gaps(code)[:4])
+        checked += any(m.startswith("v_mfma") for _, m, _ in code)
+    assert checked >= 50, f"expected the MFMA kernels, checked {checked}"
+
+
+def test_valu_mfma_gap_check_rejects_a_planted_hazard():
+    """Accepted with two instructions (or s_nop 1) between the write and the MFMA; rejected with one or none."""
+    def prog(between: list[tuple[str, str]]) -> list[tuple[int, str, str]]:
+        code = [("v_and_or_b32", "v44, v12, s68, v37")] + between + \
+            [("v_mfma_f32_16x16x32_bf16", "v[52:55], v[56:59], v[44:47], v[52:55]"), ("s_endpgm", "")]
+        return [(0x1000 + 4 * i, m, o) for i, (m, o) in enumerate(code)]
+
+    nop = ("v_perm_b32", "v12, v11, v40, s67")
+    assert not _valu_to_mfma_gaps(prog([nop, nop]))
+    assert not _valu_to_mfma_gaps(prog([("s_nop", "1")]))
+    assert _valu_to_mfma_gaps(prog([nop])) == [(0, 1)]
+    assert _valu_to_mfma_gaps(prog([])) == [(0, 0)]
