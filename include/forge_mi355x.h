@@ -160,7 +160,8 @@ int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int s
  *   cfg      NULL (policy: decode GEMV for 1..2 rows and 3..4 over N <= 8192 and K < 8192; LDS-ring kernel for
  *            17..64 rows and for 3..16 over N >= 16384 or K >= 8192; skinny kernel for the other rows up to 64;
  *            then the prefill kernels: from 256 rows the ping-pong kernel once the problem has >= 160 tiles of
- *            256 x 256, else the all-rounder) or impl FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny
+ *            256 x 256, below that the ping-pong kernel with K split 2 or 4 ways when tiles x splits reaches 160,
+ *            else the all-rounder) or impl FG_W4_GEMV (split-K decode GEMV, M <= 4), FG_W4_MFMA (skinny
  *            kernel, M <= 64), FG_W4_PREFILL / FG_W4_DEQUANT_GEMM (the prefill kernels; tile_n = 256 / 64 forces
  *            the ping-pong / all-round kernel), FG_W4_GENERIC (any shape); split_k for the prefill kernels
  *   workspace  fg_w8a16_workspace_bytes bytes (split-K partials of the prefill kernels or, under the policy, of the
