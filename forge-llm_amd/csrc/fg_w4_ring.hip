@@ -23,9 +23,10 @@
 // barrier has made them visible (the last step's after one more barrier at the end).
 //
 // K splits (KS > 1): each split writes its fp32 partial to the caller's workspace [KS, M, N] and w4_ring_reduce_kernel
-// sums them in split order (bit-reproducible), adds the bias and rounds, eight outputs per thread.  (Letting the last
-// split of a group reduce instead needs a device-scope release per workgroup, an L2 writeback that measured 60-100x
-// slower than the second launch.)
+// sums them in split order (bit-reproducible), adds the bias and rounds, four outputs per thread.  (Letting the last
+// split of a group reduce instead measured slower both ways it was built: with a device-scope release per workgroup,
+// an L2 writeback, 60-100x; with partials stored and re-read at device scope and an arrival counter, 1.2-6 us per
+// call, the last workgroup's store, atomic and load round trips running in series.)
 //
 // Requirements (w4_ring_ok): M <= 64, N % 16 == 0, K % 128 == 0, group size % 128 == 0 or one group, 16-bit scales
 // with lds even and 4-byte aligned scales / zeros, 16-byte aligned x with ldx % 8 == 0, 16-byte aligned qweight with
@@ -393,50 +394,43 @@ __global__ void __launch_bounds__(BW * kWave) w8a16_ring_kernel(RingArgs a) {
   ring_body<MB, T, BW, S, XBF16, SBF16, 2>(a);
 }
 
-// y[m, n .. n + 7] = sum over the KS partials in split order (+ bias), one thread per 8 outputs (N % 16 == 0).  The
-// partials are loaded four splits at a time before any is added (a loop that adds each split as it arrives waits out
-// one L2 round trip per split: 4.2 us for 4 splits of a 64 x 4096 output), then summed in split order.
+// y[m, n .. n + 3] = sum over the KS partials in split order (+ bias), one thread per 4 outputs (N % 16 == 0).  The
+// partials are loaded eight splits at a time before any is added (a loop that adds each split as it arrives waits out
+// one round trip per split: 4.2 us for 4 splits of a 64 x 4096 output), then summed in split order.  Four outputs per
+// thread rather than eight: twice the workgroups for the short outputs of 16 rows, and with the plans' K splits (at
+// most 8) every load of a thread in one round trip.
 template <bool XBF16>
 __global__ void __launch_bounds__(256) w4_ring_reduce_kernel(const float* __restrict__ part, int KS, int M, int N,
                                                              const void* __restrict__ bias, int bdt,
                                                              uint16_t* __restrict__ y, int64_t ldy, int vec_store) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 8 outputs
-  const int n8 = N / 8;
-  if (idx >= (int64_t)M * n8) return;
-  const int m = (int)(idx / n8), n = (int)(idx - (int64_t)m * n8) * 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 4 outputs
+  const int n4 = N / 4;
+  if (idx >= (int64_t)M * n4) return;
+  const int m = (int)(idx / n4), n = (int)(idx - (int64_t)m * n4) * 4;
   const int64_t MN4 = (int64_t)M * N / 4;
-  f32x4_rg_t a = f32x4_rg_t{0.f, 0.f, 0.f, 0.f}, b = a;
+  f32x4_rg_t acc = f32x4_rg_t{0.f, 0.f, 0.f, 0.f};
   const f32x4_rg_t* p = reinterpret_cast<const f32x4_rg_t*>(part + (int64_t)m * N + n);
-  for (int k = 0; k < KS; k += 4) {
-    f32x4_rg_t va[4], vb[4];
+  for (int k = 0; k < KS; k += 8) {
+    f32x4_rg_t v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {  // past the last split: re-read it, and add nothing below
-      const int64_t o = (int64_t)min(k + u, KS - 1) * MN4;
-      va[u] = p[o];
-      vb[u] = p[o + 1];
-    }
+    for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)min(k + u, KS - 1) * MN4];  // past the last split: re-read it
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (k + u < KS) {
-        a += va[u];
-        b += vb[u];
-      }
-    }
+    for (int u = 0; u < 8; ++u)
+      if (k + u < KS) acc += v[u];  // ... and add nothing
   }
-  float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  uint16_t h[8];
+  uint16_t h[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    if (bias) v[e] += load_f(bias, bdt, n + e);
-    h[e] = XBF16 ? f32_to_bf16_bits_hw(v[e]) : f32_to_f16_bits(v[e]);
+  for (int e = 0; e < 4; ++e) {
+    float v = acc[e];
+    if (bias) v += load_f(bias, bdt, n + e);
+    h[e] = XBF16 ? f32_to_bf16_bits_hw(v) : f32_to_f16_bits(v);
   }
   uint16_t* yr = y + (int64_t)m * ldy + n;
   if (vec_store) {
-    *reinterpret_cast<uint4*>(yr) = make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
-                                               h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+    *reinterpret_cast<uint2*>(yr) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) yr[e] = h[e];
+    for (int e = 0; e < 4; ++e) yr[e] = h[e];
   }
 }
 
@@ -508,8 +502,8 @@ size_t w4_ring_workspace_bytes(bool portable, int M, int N, int K) {
 
 static hipError_t launch_ring_reduce(bool xbf16, const float* part, int KS, int M, int N, const void* bias, int bdt,
                                      void* y, int64_t ldy, hipStream_t s) {
-  const int64_t groups = (int64_t)M * (N / 8);
-  const int vec = (reinterpret_cast<uintptr_t>(y) % 16) == 0 && (ldy % 8) == 0;
+  const int64_t groups = (int64_t)M * (N / 4);
+  const int vec = (reinterpret_cast<uintptr_t>(y) % 8) == 0 && (ldy % 4) == 0;
   const dim3 grid((unsigned)((groups + 255) / 256));
   if (xbf16) {
     hipLaunchKernelGGL(w4_ring_reduce_kernel<true>, grid, dim3(256), 0, s, part, KS, M, N, bias, bdt,
