@@ -209,12 +209,55 @@ __global__ void __launch_bounds__(256) w4_splitk_reduce_kernel(const float* __re
   y[(int64_t)m * ldy + n] = XBF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
 }
 
+// The same sum, four outputs of one row per thread (N % 4 == 0, 16-byte aligned partials): 16-byte loads of eight
+// splits in flight, one 8-byte store when y allows it.  Bit-identical to the one-output form.
+template <bool XBF16>
+__global__ void __launch_bounds__(256) w4_splitk_reduce4_kernel(const float* __restrict__ ws, int S, int M, int N,
+                                                                const void* __restrict__ bias, int bdt,
+                                                                uint16_t* __restrict__ y, int64_t ldy, int vec_store) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // group of 4 outputs
+  const int64_t MN = (int64_t)M * N;
+  if (t * 4 >= MN) return;
+  const f32x4_t* p = reinterpret_cast<const f32x4_t*>(ws) + t;
+  f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; s += 8) {
+    f32x4_t q[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) q[u] = p[(int64_t)min(s + u, S - 1) * (MN / 4)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s + u < S) v += q[u];
+  }
+  const int m = (int)(t * 4 / N), n = (int)(t * 4 - (int64_t)m * N);
+  uint16_t h[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float o = v[e];
+    if (bias) o += load_f(bias, bdt, n + e);
+    h[e] = XBF16 ? f32_to_bf16_bits(o) : f32_to_f16_bits(o);
+  }
+  uint16_t* yr = y + (int64_t)m * ldy + n;
+  if (vec_store) {
+    *reinterpret_cast<uint2*>(yr) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yr[e] = h[e];
+  }
+}
+
 template <bool XBF16>
 hipError_t launch_w4_splitk_reduce(const float* ws, int S, int M, int N, const void* bias, int bdt, void* y,
                                    int64_t ldy, hipStream_t s) {
   const int64_t MN = (int64_t)M * N;
-  hipLaunchKernelGGL(w4_splitk_reduce_kernel<XBF16>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s, ws, S, M, N,
-                     bias, bdt, static_cast<uint16_t*>(y), ldy);
+  if (N % 4 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
+    const int vec = reinterpret_cast<uintptr_t>(y) % 8 == 0 && ldy % 4 == 0;
+    hipLaunchKernelGGL(w4_splitk_reduce4_kernel<XBF16>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, s, ws,
+                       S, M, N, bias, bdt, static_cast<uint16_t*>(y), ldy, vec);
+  } else {
+    hipLaunchKernelGGL(w4_splitk_reduce_kernel<XBF16>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s, ws, S, M,
+                       N, bias, bdt, static_cast<uint16_t*>(y), ldy);
+  }
   return hipGetLastError();
 }
 template hipError_t launch_w4_splitk_reduce<true>(const float*, int, int, int, const void*, int, void*, int64_t,
