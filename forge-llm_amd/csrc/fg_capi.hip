@@ -115,6 +115,11 @@ hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, 
                                 const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
                                 int K, int gs, bool single_group, hipStream_t s);
 bool w4_gemv_split_ok(int mt, int N, int K);
+bool w4_gemv_sz8_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales8, int sdt, int M,
+                    int N, int K, int gs);
+hipError_t launch_w4_gemv_sz8(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                              const void* scales8, int sdt, const int32_t* zeros8, const void* bias, int bdt, void* y,
+                              int64_t ldy, int M, int N, int K, int gs, bool single_group, hipStream_t s);
 bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* perm, const void* scales, int sdt,
                              int64_t lds, int64_t ldq, const int32_t* zeros, int64_t ldz, int M, int N, int K, int gs,
                              bool single_group);
@@ -656,6 +661,37 @@ int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* 
                                        bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1, (int)G,
                                        static_cast<hipStream_t>(stream)),
                     "fg_w4a16_gemm_cdna4 launch");
+}
+
+int fg_w4a16_gemv_sz8(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                      const void* scales8, int scale_dtype, const int32_t* zeros8, const void* bias, int bias_dtype,
+                      void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t n_groups,
+                      fg_stream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim)
+    return fail(FG_EINVAL, "fg_w4a16_gemv_sz8: bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                (long long)K);
+  if (M == 0) return FG_OK;
+  if (x_dtype != FG_BF16 && x_dtype != FG_F16) return fail(FG_EUNSUPPORTED, "fg_w4a16_gemv_sz8: x must be bf16 or fp16");
+  if (scale_dtype != FG_F16 && scale_dtype != FG_BF16)
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemv_sz8: scales must be fp16 or bf16");
+  if (bias && !is_float_dt(bias_dtype)) return fail(FG_EINVAL, "fg_w4a16_gemv_sz8: bad bias dtype %d", bias_dtype);
+  if (!x || !qweight || !scales8 || !y) return fail(FG_EINVAL, "fg_w4a16_gemv_sz8: null tensor");
+  const int gs = group_size > 0 ? group_size : (int)K;
+  const int64_t G = (K + gs - 1) / gs;
+  if (ldq < (K + 7) / 8 || ldx < K || ldy < N) return fail(FG_EINVAL, "fg_w4a16_gemv_sz8: leading dimensions too small");
+  // the blocked arrays hold exactly the groups K needs: [N / 8][G][8] scales, [N / 8][G] zero words
+  if (n_groups != G)
+    return fail(FG_EINVAL, "fg_w4a16_gemv_sz8: n_groups=%d, but K=%lld with group %d has %lld", n_groups,
+                (long long)K, gs, (long long)G);
+  if (!fg::w4_gemv_sz8_ok(x, ldx, qweight, ldq, scales8, scale_dtype, (int)M, (int)N, (int)K, group_size))
+    return fail(FG_EUNSUPPORTED, "fg_w4a16_gemv_sz8: needs M <= 4, N %% 8 == 0, K %% 32 == 0, group %% 32 == 0 (or one "
+                                 "group), 16-byte aligned x / qweight / scales, ldx %% 8 == 0, ldq %% 4 == 0 and a "
+                                 "split-GEMV plan for the shape");
+  const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  return hip_status(fg::launch_w4_gemv_sz8(mt, x_dtype == FG_BF16, x, ldx, qweight, ldq, scales8, scale_dtype, zeros8,
+                                           bias, bias_dtype, y, ldy, (int)M, (int)N, (int)K, gs, G == 1,
+                                           static_cast<hipStream_t>(stream)),
+                    "fg_w4a16_gemv_sz8 launch");
 }
 
 int fg_w4_dequant(const int32_t* qweight, int64_t ldq, const void* scales, int scale_dtype, int64_t lds,

@@ -475,7 +475,9 @@ __global__ void __launch_bounds__(w4_tile_max_waves(MT, S) * kWave) w4_gemv_tile
 
 
 // ------------------------------------------------------------------------------------------------ GEMV (split-K)
-enum { kSplitGeneral = 0, kSplitF16Scales = 1, kSplitBf16Scales = 2 };  // w4_gemv_split_kernel MODE
+// w4_gemv_split_kernel MODE: the scale type of the FAST forms, plus kSplitSz8 for scales / zero words blocked by 8
+// channels ([N / 8][G][8] 16-bit scales, [N / 8][G] zero words) instead of the portable [G, lds] / [G, ldz]
+enum { kSplitGeneral = 0, kSplitF16Scales = 1, kSplitBf16Scales = 2, kSplitSz8 = 4 };
 // Decode GEMV for M <= MT <= 4 with no LDS on the hot path.  A wavefront owns R consecutive output channels and one K
 // slice of at most S 32-column chunks per lane (chunk c = slice start + lane + 64 i); the K slices of a channel block
 // are the KS wavefronts of one workgroup, summed in a fixed order through LDS at the end.  The lane's x chunks are read
@@ -503,6 +505,7 @@ struct SplitArgs {
   int gs32;       // group size / 32, 0 for one group per row
   uint32_t gmul;  // group of chunk c = umulhi(c, gmul) when gs32 > 1 (floor((2^32 - 1) / gs32) + 1)
   uint32_t qbytes, xbytes, sbytes, zbytes;  // FAST: byte spans of qweight, x, scales, zeros (each < 2^32)
+  uint32_t sz8_block;  // kSplitSz8: bytes of one 8-channel block of scales (G * 16)
 };
 
 // Workgroup: blockDim.x = 64 * BW (one wavefront per channel block), blockDim.y = KS (one row of wavefronts per K
@@ -514,7 +517,8 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
     int hasz, const void* __restrict__ bias, int bdt, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
     SplitArgs a) {
   static_assert(R * MT == 4 || R * MT == 8 || R * MT == 16, "rows x batch must be 4, 8 or 16");
-  constexpr bool FAST = MODE != kSplitGeneral;
+  constexpr bool FAST = MODE != kSplitGeneral, SZ8 = (MODE & kSplitSz8) != 0;
+  constexpr int SM = MODE & 3;  // scale type
   constexpr uint32_t kMagicBytes = XBF16 ? 0x43434343u : 0x64646464u;
   constexpr uint32_t kOnes = XBF16 ? 0x3f803f80u : 0x3c003c00u;  // (1, 1) as bf16 / fp16 pairs
   constexpr float kB = XBF16 ? 128.f : 1024.f;
@@ -577,7 +581,26 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int64_t srow = (int64_t)gl[i] * lds;
-      if constexpr (FAST) {  // group row gl * lds (per lane, < 2^24 each) + the block's first channel (uniform)
+      if constexpr (SZ8) {  // group gl's 16 bytes (per lane) in the blocks of the wavefront's channels (uniform)
+        const uint32_t sv = (uint32_t)gl[i] * 16u, b8 = (uint32_t)nr / 8u;
+        if constexpr (R == 4) {
+          const uint2 t = buf_ld8(rs, sv, b8 * a.sz8_block + (uint32_t)(nr & 7) * 2u);
+          sraw[i][0] = t.x;
+          sraw[i][1] = t.y;
+        } else {
+#pragma unroll
+          for (int h = 0; h < R / 8; ++h) {
+            const uint4 t = buf_ld16(rs, sv, (b8 + (uint32_t)h) * a.sz8_block);
+            sraw[i][4 * h] = t.x;
+            sraw[i][4 * h + 1] = t.y;
+            sraw[i][4 * h + 2] = t.z;
+            sraw[i][4 * h + 3] = t.w;
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < (R + 7) / 8; ++h)
+          zw[i][h] = buf_ld4(rz, (uint32_t)gl[i] * 4u, (b8 + (uint32_t)h) * (a.sz8_block / 4u));
+      } else if constexpr (FAST) {  // group row gl * lds (per lane, < 2^24 each) + the block's first channel (uniform)
         const uint32_t sv = __umul24((uint32_t)gl[i], (uint32_t)lds) * 2u;
         if constexpr (R == 4) {
           const uint2 t = buf_ld8(rs, sv, (uint32_t)nr * 2u);
@@ -661,9 +684,9 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float sc;
-      if constexpr (MODE == kSplitF16Scales) {
+      if constexpr (SM == kSplitF16Scales) {
         sc = f16_bits_to_f32((uint16_t)((r & 1) ? sraw[i][r >> 1] >> 16 : sraw[i][r >> 1]));
-      } else if constexpr (MODE == kSplitBf16Scales) {
+      } else if constexpr (SM == kSplitBf16Scales) {
         sc = __uint_as_float((r & 1) ? sraw[i][r >> 1] & 0xffff0000u : sraw[i][r >> 1] << 16);
       } else {
         sc = raw_bits_to_f32(sraw[i][r], sdt);
@@ -751,10 +774,10 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
 }
 
 template <int MT, int S, int R, bool XBF16>
-static hipError_t launch_split_t(bool fast, const void* x, int64_t ldx, const int32_t* perm, const int32_t* qw,
-                                 int64_t ldq, const void* scales, int sdt, int64_t lds, const int32_t* zeros,
-                                 int64_t ldz, const void* bias, int bdt, void* y, int64_t ldy, int M, int N, int K,
-                                 int gs32, int KS, int BW, hipStream_t s) {
+static hipError_t launch_split_t(bool fast, bool sz8, const void* x, int64_t ldx, const int32_t* perm,
+                                 const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
+                                 const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y, int64_t ldy,
+                                 int M, int N, int K, int gs32, int KS, int BW, hipStream_t s) {
   const int nblk = (N + R - 1) / R;
   const int hasz = zeros != nullptr;
   // symmetric weights: the zero word is read from qweight (always valid memory) and ignored
@@ -769,26 +792,32 @@ static hipError_t launch_split_t(bool fast, const void* x, int64_t ldx, const in
   // byte spans for the FAST buffer loads (split_fast checked each is < 2^32; unused by the general form)
   a.qbytes = fast ? (uint32_t)((int64_t)N * ldq * 4) : 0u;
   a.xbytes = fast ? (uint32_t)((int64_t)M * ldx * 2) : 0u;
-  a.sbytes = fast ? (uint32_t)(G * lds * 2) : 0u;
-  a.zbytes = fast ? (hasz ? (uint32_t)(G * ldz * 4) : a.qbytes) : 0u;
+  // sz8: [N / 8][G][8] scales and [N / 8][G] zero words (split_sz8_ok checked N % 8 == 0 and the spans)
+  a.sbytes = fast ? (uint32_t)(G * (sz8 ? N : lds) * 2) : 0u;
+  a.zbytes = fast ? (hasz ? (uint32_t)(G * (sz8 ? N / 8 : ldz) * 4) : a.qbytes) : 0u;
+  a.sz8_block = (uint32_t)(G * 16);
   const dim3 grid((nblk + BW - 1) / BW), block(kWave * BW, KS);
+  const bool bf = sdt == FG_BF16;
   auto kern = !fast ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitGeneral>
-                    : (sdt == FG_BF16 ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales>
-                                      : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales>);
-  note_kernel("w4_gemv_split_kernel<%d,%d,%d,%s>%s KS=%d", MT, S, R, XBF16 ? "bf16" : "f16", fast ? "" : " general", KS);
+              : sz8 ? (bf ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales | kSplitSz8>
+                          : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales | kSplitSz8>)
+                    : (bf ? w4_gemv_split_kernel<MT, S, R, XBF16, kSplitBf16Scales>
+                          : w4_gemv_split_kernel<MT, S, R, XBF16, kSplitF16Scales>);
+  note_kernel("w4_gemv_split_kernel<%d,%d,%d,%s>%s KS=%d", MT, S, R, XBF16 ? "bf16" : "f16",
+              !fast ? " general" : (sz8 ? " sz8" : ""), KS);
   hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const uint16_t*>(x), ldx, perm, qw, ldq, scales, sdt, lds, zp,
                      ldzp, hasz, bias, bdt, static_cast<uint16_t*>(y), ldy, M, N, K, a);
   return hipGetLastError();
 }
 
 template <bool XBF16>
-static hipError_t launch_split_x(int mt, int S, int R, bool fast, const void* x, int64_t ldx, const int32_t* perm,
-                                 const int32_t* qw, int64_t ldq, const void* scales, int sdt, int64_t lds,
-                                 const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y, int64_t ldy,
-                                 int M, int N, int K, int gs32, int KS, int BW, hipStream_t s) {
-#define FG_SPLIT(MT_, S_, R_)                                                                                       \
-  return launch_split_t<MT_, S_, R_, XBF16>(fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, \
-                                            ldy, M, N, K, gs32, KS, BW, s)
+static hipError_t launch_split_x(int mt, int S, int R, bool fast, bool sz8, const void* x, int64_t ldx,
+                                 const int32_t* perm, const int32_t* qw, int64_t ldq, const void* scales, int sdt,
+                                 int64_t lds, const int32_t* zeros, int64_t ldz, const void* bias, int bdt, void* y,
+                                 int64_t ldy, int M, int N, int K, int gs32, int KS, int BW, hipStream_t s) {
+#define FG_SPLIT(MT_, S_, R_)                                                                                        \
+  return launch_split_t<MT_, S_, R_, XBF16>(fast, sz8, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, \
+                                            y, ldy, M, N, K, gs32, KS, BW, s)
   if (mt == 1) {
     if (S == 2) FG_SPLIT(1, 2, 4);
     if (R == 4) FG_SPLIT(1, 1, 4);
@@ -821,10 +850,38 @@ hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, 
   const int gs32 = single_group ? 0 : gs / 32;
   const bool fast = split_fast(R, x, ldx, perm, scales, sdt, lds, ldq, zeros ? ldz : 0, M, N, K, gs32);
   if (xbf16)
-    return launch_split_x<true>(mt, S, R, fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy,
-                                M, N, K, gs32, KS, BW, s);
-  return launch_split_x<false>(mt, S, R, fast, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt, y, ldy,
-                               M, N, K, gs32, KS, BW, s);
+    return launch_split_x<true>(mt, S, R, fast, false, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt,
+                                y, ldy, M, N, K, gs32, KS, BW, s);
+  return launch_split_x<false>(mt, S, R, fast, false, x, ldx, perm, qw, ldq, scales, sdt, lds, zeros, ldz, bias, bdt,
+                               y, ldy, M, N, K, gs32, KS, BW, s);
+}
+
+// The split GEMV's branch-free form reading scales / zero words blocked by 8 channels ([N / 8][G][8] 16-bit scales,
+// [N / 8][G] zero words): each wavefront's scales and zero words of a K slice are one contiguous run instead of one
+// strided word per group.
+bool w4_gemv_sz8_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, const void* scales8, int sdt, int M,
+                    int N, int K, int gs) {
+  int S, R, KS, BW;
+  const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  if (M < 1 || M > 4 || !w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return false;
+  const int gs32 = gs > 0 ? gs / 32 : 0;
+  if ((gs > 0 && gs % 32 != 0) || N % 8 != 0 || (reinterpret_cast<uintptr_t>(qw) % 16) != 0 || (ldq % 4) != 0)
+    return false;
+  // the portable form's checks with the blocked arrays' strides (N per group row of scales, N / 8 of zero words)
+  return split_fast(R, x, ldx, nullptr, scales8, sdt, N, ldq, N / 8, M, N, K, gs32);
+}
+
+hipError_t launch_w4_gemv_sz8(int mt, bool xbf16, const void* x, int64_t ldx, const int32_t* qw, int64_t ldq,
+                              const void* scales8, int sdt, const int32_t* zeros8, const void* bias, int bdt, void* y,
+                              int64_t ldy, int M, int N, int K, int gs, bool single_group, hipStream_t s) {
+  int S, R, KS, BW;
+  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return hipErrorInvalidValue;
+  const int gs32 = single_group ? 0 : gs / 32;
+  if (xbf16)
+    return launch_split_x<true>(mt, S, R, true, true, x, ldx, nullptr, qw, ldq, scales8, sdt, N, zeros8, N / 8, bias,
+                                bdt, y, ldy, M, N, K, gs32, KS, BW, s);
+  return launch_split_x<false>(mt, S, R, true, true, x, ldx, nullptr, qw, ldq, scales8, sdt, N, zeros8, N / 8, bias,
+                               bdt, y, ldy, M, N, K, gs32, KS, BW, s);
 }
 
 bool w4_gemv_split_ok(int mt, int N, int K) {

@@ -65,6 +65,7 @@ SIGNATURES = {
     "fg_w4a16_gemm_cdna4": ([P, I64, INT, P, I64, P, INT, I64, P, I64, P, INT, P, I64, I64, I64, I64, I32_, I32_, P,
                              SZ, P], INT),
     "fg_w4a16_cdna4_workspace_bytes": ([I64, I64, I64, I32_], SZ),
+    "fg_w4a16_gemv_sz8": ([P, I64, INT, P, I64, P, INT, P, P, INT, P, I64, I64, I64, I64, I32_, I32_, P], INT),
     "fg_w4a16_workspace_bytes": ([I64, I64, I64, I32_, I32_, I32_, I32_, ctypes.POINTER(W4Config)], SZ),
     "fg_w4_dequant": ([P, I64, P, INT, I64, P, I64, P, P, INT, I64, I64, I64, I32_, I32_, P], INT),
     "fg_w8a16_gemm": ([P, I64, INT, P, I64, P, INT, I64, P, INT, P, I64, I64, I64, I64, I32_, I32_,

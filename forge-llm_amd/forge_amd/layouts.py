@@ -510,6 +510,22 @@ def repack(p: PackedW4, new_layout: Layout | str) -> PackedW4:
     return pack_w4(q, s, z, p.group_size, lay, p.g_idx)
 
 
+def sz8_blocks(scales: torch.Tensor, zeros: torch.Tensor | None, n: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """A portable_row weight's scales ``[G, >= N]`` and zero words ``[G, >= N / 8]`` re-blocked by 8 channels for the
+    decode GEMV's contiguous reads (``fg_w4a16_gemv_sz8``): ``scales8 [N / 8, G, 8]`` with scale ``(g, n)`` at
+    ``[n // 8, g, n % 8]``, ``zeros8 [N / 8, G]`` with the zero word of group ``g`` and channels ``8 b .. 8 b + 7`` at
+    ``[b, g]``.  A permutation of the stored values on their device (no arithmetic); ``zeros`` None stays None."""
+    if n % 8:
+        raise ConfigError(f"8-channel scale blocks need N % 8 == 0, got N={n}")
+    if scales.dim() != 2 or scales.shape[1] < n or (zeros is not None and zeros.shape[1] < n // 8):
+        raise ConfigError(f"scales {tuple(scales.shape)} / zeros {None if zeros is None else tuple(zeros.shape)} do "
+                          f"not cover N={n}")
+    g = scales.shape[0]
+    s8 = scales[:, :n].reshape(g, n // 8, 8).permute(1, 0, 2).contiguous()
+    z8 = None if zeros is None else zeros[:, :n // 8].t().contiguous()
+    return s8, z8
+
+
 def require_portable(p: PackedW4) -> None:
     if p.layout.kind != KIND_PORTABLE:
         raise ConfigError(f"this kernel reads the portable_row layout, got {p.layout_id}; repack() first")
@@ -816,6 +832,6 @@ __all__ = [
     "effective_group", "fragment_layout", "fragment_tile_perm", "get_layout", "known_layouts", "num_groups",
     "pack_nibbles_int32", "pack_simple_int4", "pack_w4", "pack_w4_from_simple", "pack_w8", "portable_layout",
     "quantize_fp8_weight", "quantize_int8_weight", "quantize_w4_rtn", "quantize_w8_rtn", "register_layout", "repack", "require_portable", "roundup",
-    "sort_columns_by_group", "unpack_nibbles_int32", "unpack_simple_int4", "unpack_w4", "unpack_w8",
+    "sort_columns_by_group", "sz8_blocks", "unpack_nibbles_int32", "unpack_simple_int4", "unpack_w4", "unpack_w8",
     "w4_storage_shapes",
 ]

@@ -50,6 +50,7 @@ from .layouts import (
     quantize_w4_rtn,
     quantize_w8_rtn,
     repack,
+    sz8_blocks,
     w4_storage_shapes,
 )
 
@@ -314,6 +315,55 @@ def prepare_w4(packed: PackedW4, layout: Layout | str | None = None) -> PackedW4
     return p
 
 
+# Rows for which a portable_row weight's 8-channel scale blocks (kept by KernelW4A16Linear.prepare) serve the call:
+# the split-K decode GEMV's, which reads them as one contiguous run per wavefront and K slice (graph replays over a
+# 1.2 GB ring, M = 1, us, portable / blocked: qkv 5.13 / 4.89, o_proj 4.31 / 4.26, gate+up 13.84 / 12.91, down 9.16 /
+# 8.59; M = 2 down 11.29 / 10.15), bit-identical results.
+SZ8_ROWS = 2
+_SZ8_KEY = "hip.sz8"  # p.meta entry: (tensor stamp, scales8, zeros8)
+
+
+def _stamp(packed: PackedW4) -> tuple:
+    return tuple((t.data_ptr(), t._version) for t in packed.tensors().values())
+
+
+def prepare_w4_sz8(packed: PackedW4) -> bool:
+    """Keep ``packed``'s scales and zero words re-blocked by 8 channels (``layouts.sz8_blocks``) in ``packed.meta``
+    for the 1..2-row decode GEMV; True when made (a portable_row weight on the GPU with N % 8 == 0, K % 32 == 0, a
+    group size that is a multiple of 32 or one group, 16-bit scales, no g_idx).  Outside graph capture."""
+    if not _sz8_eligible(packed):
+        return False
+    s8, z8 = sz8_blocks(packed.scales, packed.zeros, packed.n)
+    packed.meta[_SZ8_KEY] = (_stamp(packed), s8, z8)
+    return True
+
+
+def _sz8_eligible(p: PackedW4) -> bool:
+    return (p.layout.kind == KIND_PORTABLE and p.qweight.is_cuda and p.g_idx is None and p.n % 8 == 0
+            and p.k % 32 == 0 and (p.group_size <= 0 or p.group_size >= p.k or p.group_size % 32 == 0)
+            and p.scales.dtype in (torch.float16, torch.bfloat16) and p.num_groups == num_groups(p.k, p.group_size))
+
+
+def _sz8_copy(packed: PackedW4) -> tuple[torch.Tensor, torch.Tensor | None] | None:
+    """The 8-channel scale blocks kept beside a portable_row weight, if made and its tensors have not changed."""
+    hit = packed.meta.get(_SZ8_KEY) if packed.meta is not None else None
+    return (hit[1], hit[2]) if hit is not None and hit[0] == _stamp(packed) else None
+
+
+def _w4_sz8_call(x2: torch.Tensor, p: PackedW4, blocks: tuple[torch.Tensor, torch.Tensor | None],
+                 bias: torch.Tensor | None, y: torch.Tensor) -> bool:
+    """The decode GEMV on the 8-channel scale blocks; False (nothing launched) when x's alignment rules it out."""
+    if _ld(x2) % 8 or x2.data_ptr() % 16 or _ld(p.qweight) % 4 or p.qweight.data_ptr() % 16:
+        return False
+    m, k = x2.shape
+    s8, z8 = blocks
+    _check(_lib.lib().fg_w4a16_gemv_sz8(
+        _lib.ptr(x2), _ld(x2), _lib.dtype_code(x2.dtype), _lib.ptr(p.qweight), _ld(p.qweight), _lib.ptr(s8),
+        _lib.dtype_code(s8.dtype), _lib.ptr(z8), _lib.ptr(bias), _code_or_zero(bias), _lib.ptr(y), y.stride(0), m, p.n,
+        k, p.group_size, p.num_groups, _lib.stream_of(x2)), "fg_w4a16_gemv_sz8")
+    return True
+
+
 @dataclass
 class _W4Operands:
     weight: PackedW4
@@ -418,7 +468,11 @@ def w4a16_linear(x: torch.Tensor, packed: PackedW4, bias: torch.Tensor | None = 
         b = None if bias is None else bias.contiguous()
         copy = (_cdna4_copy(packed) if packed.layout.kind == KIND_PORTABLE
                 and CDNA4_COPY_ROWS[0] <= m <= CDNA4_COPY_ROWS[1] else None)
-        if copy is not None and _cdna4_fits(copy, m, config):
+        blocks = (_sz8_copy(packed) if packed.layout.kind == KIND_PORTABLE and m <= SZ8_ROWS and config is None
+                  and forced_impl() is None else None)
+        if blocks is not None and _w4_sz8_call(x2, packed, blocks, b, y):
+            pass
+        elif copy is not None and _cdna4_fits(copy, m, config):
             _w4_cdna4_call(x2, copy, b, y)
         elif _cdna4_fits(packed, m, config):
             _w4_cdna4_call(x2, packed, b, y)
@@ -878,17 +932,22 @@ class KernelW4A16Linear(_PackedLinear):
     def prepare(self) -> KernelW4A16Linear:
         """Host-synchronising preparation (repack, act-order sort) done now, so forward never syncs; runs after
         ``load_state_dict`` and ``.to()``.  On the GPU a portable_row weight also gets a CDNA4-layout copy for 3..64-row
-        calls (``CDNA4_COPY_ROWS``; the state dict stays portable_row; ``FORGE_W4_CDNA4_COPY=0`` turns it off)."""
+        calls (``CDNA4_COPY_ROWS``) and its scales / zero words blocked by 8 channels for 1..2-row calls
+        (``SZ8_ROWS``); the state dict stays portable_row (``FORGE_W4_CDNA4_COPY=0`` / ``FORGE_W4_SZ8_COPY=0`` turn
+        the copies off)."""
         if self.g_idx is not None or self.layout.kind != KIND_PORTABLE:
             try:
                 prepare_w4(self.packed())
             except (ConfigError, RuntimeError) as e:  # forward prepares lazily outside capture
                 log.debug("W4 prepare deferred: %s", e)
-        elif self._cdna4_copy_wanted():
-            try:
-                prepare_w4(self.packed(), CDNA4_W4)
-            except (ConfigError, RuntimeError) as e:
-                log.debug("W4 CDNA4 copy not made: %s", e)
+        else:
+            if self._cdna4_copy_wanted():
+                try:
+                    prepare_w4(self.packed(), CDNA4_W4)
+                except (ConfigError, RuntimeError) as e:
+                    log.debug("W4 CDNA4 copy not made: %s", e)
+            if os.environ.get("FORGE_W4_SZ8_COPY", "1") != "0":
+                prepare_w4_sz8(self.packed())
         return self
 
     def _cdna4_copy_wanted(self) -> bool:
@@ -1065,6 +1124,6 @@ def make_packed_linear(kind: str, linear: nn.Linear | None = None, *, packed: Pa
 __all__ = [
     "KernelFp8Linear", "KernelInt8Linear", "KernelW4A16Linear", "KernelW8A16Linear", "PACKED_LINEAR_CLASSES",
     "device_selftest", "force_ref", "forced_impl", "fp8_linear", "int8_gemm", "int8_linear", "kernel_debug",
-    "kernel_strict", "last_kernel", "last_path", "make_packed_linear", "prepare_fp8_scales", "prepare_w4", "quantize_act_fp8",
+    "kernel_strict", "last_kernel", "last_path", "make_packed_linear", "prepare_fp8_scales", "prepare_w4", "prepare_w4_sz8", "quantize_act_fp8",
     "quantize_act_int8", "quantize_weight_fp8", "quantize_weight_int8", "reset_failure_memo", "w4_dequant", "w4a16_linear", "w8a16_linear",
 ]

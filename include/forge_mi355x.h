@@ -143,6 +143,23 @@ int fg_w4a16_gemm_cdna4(const void* x, int64_t ldx, int x_dtype, const int32_t* 
  * split). */
 size_t fg_w4a16_cdna4_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size);
 
+/* W4A16 decode GEMV (1 <= M <= 4) on portable_row weights whose scales and zero-points are re-blocked by 8 channels.
+ * No counterpart in the reference: the reference's GEMV reads the portable [G, N] scales (forge/kernels/layouts/w4.py
+ * :15-17), and this entry point serves the copy that forge_amd's packed-linear module keeps beside them
+ * (forge_amd.layouts.sz8_blocks, KernelW4A16Linear.prepare): with it each wavefront reads the scales and zero words of
+ * its channels and K slice as one contiguous run instead of one strided word per group.  Same arguments and results
+ * as fg_w4a16_gemm (split-K decode GEMV, bit-identical output) except:
+ *   scales8  fp16|bf16 [N / 8][G][8]: scale (g, n) at ((n / 8) * G + g) * 8 + n % 8
+ *   zeros8   int32 [N / 8][G]: the zero word of group g and channels 8 b .. 8 b + 7 at b * G + g (nibble n % 8 =
+ *            channel n's zero-point); NULL = symmetric (zero-point 8)
+ *   n_groups must equal ceil(K / group_size); no perm / g_idx, no workspace
+ * Needs N % 8 == 0, K % 32 == 0, group_size % 32 == 0 (or one group), 16-byte aligned x (ldx % 8 == 0), qweight
+ * (ldq % 4 == 0) and scales8; FG_EUNSUPPORTED otherwise. */
+int fg_w4a16_gemv_sz8(const void* x, int64_t ldx, int x_dtype, const int32_t* qweight, int64_t ldq,
+                      const void* scales8, int scale_dtype, const int32_t* zeros8, const void* bias, int bias_dtype,
+                      void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t n_groups,
+                      fg_stream_t stream);
+
 /* Dense dequantisation out[n,k] = (q - z) * s computed in fp32 and rounded once to out_dtype (FG_F32|FG_F16|FG_BF16).
  * Replaces forge/kernels/triton/gemm_w4_dequant.py:143-191 (w4_dequant) and PackedW4.dequantize
  * (forge/kernels/layouts/w4.py:137-140 -> dequantize_parts :294-305). */

@@ -190,3 +190,26 @@ def test_cdna4_unpack_pairs_are_mfma_b_operands():
                 v = (w >> (4 * pair)) & 0x000F000F
                 cols = 32 * s + 8 * j + 2 * pair
                 assert (v & 0xF, v >> 16) == (int(q[r, cols]), int(q[r, cols + 1]))
+
+
+@pytest.mark.parametrize("n,k,gs,sym", [(24, 256, 128, False), (4096, 512, 64, True), (40, 96, 32, False)])
+def test_sz8_blocks_is_the_documented_permutation(n, k, gs, sym):
+    """scales8[n // 8, g, n % 8] == scales[g, n] and zeros8[b, g] == zero word (g, b) for every element, checked
+    element by element against the packed portable_row tensors (the nibble n % 8 of zeros8[n // 8, g] is channel n's
+    zero-point); padding past N (scales stored wider) is dropped; N % 8 != 0 is refused."""
+    q, s, z = w4_parts(n, k, gs, sym, seed=n + k)
+    p = L.pack_w4(q, s, z, gs)
+    s8, z8 = L.sz8_blocks(p.scales, p.zeros, n)
+    G = p.scales.shape[0]
+    assert s8.shape == (n // 8, G, 8) and s8.is_contiguous() and s8.dtype == p.scales.dtype
+    for g in range(G):
+        for c in range(n):
+            assert s8[c // 8, g, c % 8].item() == p.scales[g, c].item()
+            if z is not None:
+                assert (int(z8[c // 8, g]) >> (4 * (c % 8))) & 0xF == int(z[c, g])
+    assert (z8 is None) == sym
+    # a wider stored scale row (ldz / lds padding) keeps the first N channels
+    wide = torch.cat([p.scales, torch.zeros(G, 8, dtype=p.scales.dtype)], 1)
+    assert torch.equal(L.sz8_blocks(wide, p.zeros, n)[0], s8)
+    with pytest.raises(ConfigError):
+        L.sz8_blocks(p.scales[:, :n - 4], None, n - 4)
