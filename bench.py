@@ -3,8 +3,11 @@
 Primary metric (``value``): W4A16 GEMV HBM throughput at M=1 on the Llama-3-8B decode linears.
 One *step* = every W4A16 linear of one Llama-3-8B decode token: 32 layers x {qkv (K=4096, N=6144), o_proj (4096,
 4096), gate+up (4096, 28672), down (14336, 4096)} = 128 GEMVs over 32 distinct weight sets (3.64 GB of packed weights,
-far above the 256 MB Infinity Cache, so every weight byte comes from HBM).  Inputs are resident in HBM before timing;
-the step is captured once as a HIP graph and replayed (launch overhead excluded, as a decode server runs it).
+far above the 256 MB Infinity Cache, so every weight byte comes from HBM).  Each linear runs through
+KernelW4A16Linear, the module a model loader swaps in (its prepare() keeps the scales and zero-points blocked by 8
+channels beside the portable_row tensors, which the 1..2-row GEMV reads); ``portable_row_raw_op`` times the same ring
+through w4a16_linear on the portable_row tensors alone.  Inputs are resident in HBM before timing; the step is captured
+once as a HIP graph and replayed (launch overhead excluded, as a decode server runs it).
 value = algorithmic bytes per step / step time, bytes per linear = N*K/2 + 2*G*N + G*N/2 + 2*M*K + 2*M*N
 (packed weights, fp16 scales, packed zeros, bf16 x and y; forge/kernels/bench.py:164-166).
 
@@ -51,7 +54,7 @@ LAYERS = 32
 GROUP = 128
 # the launch the C library's policy makes for gate+up at M=1: one row of x, one 16-byte chunk per lane, 8 output
 # channels per wavefront (two K slices of 2048 columns, eight channel blocks per workgroup)
-DOM_KERNEL = "w4_gemv_split_kernel<1,1,8,bf16>"
+DOM_KERNEL = "w4_gemv_split_kernel<1,1,8,bf16> sz8"  # the gate+up GEMV the packed-linear module runs at M=1
 METRIC = "W4A16 GEMV HBM GB/s (% peak) at M=1; W8A8 TFLOPS (% MFMA peak) at M=4096"
 
 
@@ -125,7 +128,7 @@ def time_eager(torch, fn, reps: int, warmup: int) -> Timing:
     return _timed_calls(torch, fn, reps)
 
 
-def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -> tuple[dict, dict]:
+def bench_w4_sweep(torch, ops, ring, mods, dev, gen, timer, steps: int, warmup: int) -> tuple[dict, dict]:
     """configs[1] decode sweep at M in {4, 16, 64} (GB/s of algorithmic bytes, HIP-graph replays over the 32-layer
     ring) and configs[2] prefill at M in {512, 2048, 8192} (TFLOP/s against bf16 dense MFMA, one weight per shape).
     The decode rows ``M4 / M16 / M64`` go through KernelW4A16Linear, the module a served model runs (portable_row
@@ -154,11 +157,8 @@ def bench_w4_sweep(torch, ops, ring, dev, gen, timer, steps: int, warmup: int) -
     for m in (4, 16, 64):
         sweep(f"M{m}_portable_row", m, portable, lambda x, p: ops.w4a16_linear(x, p))
     # the modules a model loader swaps in: the same portable_row tensors, and the CDNA4-layout copy each keeps
-    mods = [(nm, ops.KernelW4A16Linear.from_packed(p)) for nm, p in portable]
-    torch.cuda.synchronize()
     for m in (4, 16, 64):
-        sweep(f"M{m}", m, mods, lambda x, mod: mod(x))
-    del mods
+        sweep(f"M{m}", m, [(nm, mod) for nm, _, mod in mods], lambda x, mod: mod(x))
     prefill = {}
     dense = {name: torch.randn(n, k, device=dev, generator=gen).bfloat16() for name, (k, n) in SHAPES.items()}
     for m in (512, 2048, 8192):
@@ -357,7 +357,8 @@ def measure_copy_bandwidth(torch, dev, nbytes: int = 1 << 30, reps: int = 20) ->
 def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
     """Counter-pass workloads (no timing), each after a 256 MiB device-to-device copy run three times (known bytes:
     calibrates FETCH_SIZE / WRITE_SIZE):
-    gemv   -- the gate+up GEMV (K=4096, N=28672, M=1) over a ring of 32 weights, twice (64 launches);
+    gemv   -- the gate+up GEMV (K=4096, N=28672, M=1) through KernelW4A16Linear over a ring of 32 weights, twice
+              (64 launches of the 8-channel-block GEMV);
     decode -- the CDNA4-layout W4 kernel at M=16 and M=64 on the four Llama-3-8B shapes, over a ring of 6 weights per
               shape, twice (12 launches per shape and M);
     w8a8   -- the FP8 GEMM at M=4096, K=N=8192 and the INT8 GEMM at M=4096, K=8192, N=10240, 5 launches each;
@@ -372,13 +373,15 @@ def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
     if which == "gemv":
         k, n = SHAPES["gate_up"]
         x = torch.randn(1, k, device=dev, generator=gen).bfloat16()
-        ring = [make_layer_weights(torch, layouts, dev, k, n, gen) for _ in range(LAYERS)]
+        ring = [ops.KernelW4A16Linear.from_packed(make_layer_weights(torch, layouts, dev, k, n, gen))
+                for _ in range(LAYERS)]
         torch.cuda.synchronize()
         for _ in range(2):
-            for p in ring:
-                ops.w4a16_linear(x, p)
+            for mod in ring:
+                mod(x)
         torch.cuda.synchronize()
-        log("pmc workload done: 3 x 256 MiB copy, 64 gate_up GEMV launches")
+        log(f"pmc gemv: {ops.last_kernel()}")
+        log("pmc workload done: 3 x 256 MiB copy, 64 gate_up GEMV launches (packed-linear modules)")
     elif which == "decode":
         for name, (k, n) in SHAPES.items():
             ring = [layouts.repack(make_layer_weights(torch, layouts, dev, k, n, gen), layouts.CDNA4_W4)
@@ -441,7 +444,7 @@ def load_traffic() -> dict | None:
         return None
     with open(path) as f:
         tr = json.load(f)
-    return tr if tr.get("kernel", "").split(" ")[0] == DOM_KERNEL else None
+    return tr if tr.get("kernel", "").startswith(DOM_KERNEL + " ") else None
 
 
 def _cpu_model() -> str:
@@ -550,11 +553,18 @@ def main() -> None:
     for layer in range(LAYERS):
         for name, (k, n) in SHAPES.items():
             ring.append((name, xs[k], make_layer_weights(torch, layouts, dev, k, n, gen)))
+    # the modules a model loader swaps in over the same portable_row tensors: prepare() keeps the 8-channel scale
+    # blocks (1..2 rows) and the CDNA4-layout copy (3..64 rows) beside them
+    mods = [(name, x, ops.KernelW4A16Linear.from_packed(p)) for name, x, p in ring]
     torch.cuda.synchronize()
     step_bytes = sum(w4_bytes(1, p.k, p.n) for _, _, p in ring)
     log(f"ring: {len(ring)} linears, {sum(p.nbytes for _, _, p in ring) / 1e9:.2f} GB packed weights")
 
     def step():
+        for _, x, mod in mods:
+            mod(x)
+
+    def step_portable():
         for _, x, p in ring:
             ops.w4a16_linear(x, p)
 
@@ -563,22 +573,30 @@ def main() -> None:
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"step: {ms:.4f} ms (median {ms.median:.4f}, IQR {ms.iqr:.4f}), {value:.1f} GB/s "
         f"({value / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    ms_port = timer(torch, step_portable, args.steps, args.warmup)
+    log(f"step on the portable_row tensors alone (raw op): {ms_port:.4f} ms, "
+        f"{step_bytes / (ms_port * 1e-3) / 1e9:.1f} GB/s")
 
-    per_shape = {}
-    for name, (k, n) in SHAPES.items():
-        sel = [(x, p) for nm, x, p in ring if nm == name]
+    def shape_rows(items, call) -> dict:
+        rows = {}
+        for name, (k, n) in SHAPES.items():
+            sel = [(x, w) for nm, x, w in items if nm == name]
 
-        def run(sel=sel):
-            for x, p in sel:
-                ops.w4a16_linear(x, p)
+            def run(sel=sel):
+                for x, w in sel:
+                    call(x, w)
 
-        tt = timer(torch, run, args.steps, args.warmup)
-        t = tt / len(sel)
-        gbs = w4_bytes(1, k, n) / (t * 1e-3) / 1e9
-        per_shape[name] = {"K": k, "N": n, "us": round(t * 1e3, 3), "GBps": round(gbs, 1),
-                           "frac": round(gbs / HBM_PEAK_GBS, 4), "median_us": round(tt.median / len(sel) * 1e3, 3),
-                           "iqr_us": round(tt.iqr / len(sel) * 1e3, 3), "kernel": ops.last_kernel()}
-        log(f"  {name:8s} K={k:5d} N={n:5d}: {t * 1e3:8.3f} us  {gbs:7.1f} GB/s")
+            tt = timer(torch, run, args.steps, args.warmup)
+            t = tt / len(sel)
+            gbs = w4_bytes(1, k, n) / (t * 1e-3) / 1e9
+            rows[name] = {"K": k, "N": n, "us": round(t * 1e3, 3), "GBps": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "median_us": round(tt.median / len(sel) * 1e3, 3),
+                          "iqr_us": round(tt.iqr / len(sel) * 1e3, 3), "kernel": ops.last_kernel()}
+            log(f"  {name:8s} K={k:5d} N={n:5d}: {t * 1e3:8.3f} us  {gbs:7.1f} GB/s  {ops.last_kernel()}")
+        return rows
+
+    per_shape = shape_rows(mods, lambda x, mod: mod(x))
+    per_shape_portable = shape_rows(ring, lambda x, p: ops.w4a16_linear(x, p))
     copy_bw = measure_copy_bandwidth(torch, dev)
     log(f"copy bandwidth: {copy_bw['GBps']:.0f} GB/s")
     dom = per_shape["gate_up"]
@@ -601,11 +619,15 @@ def main() -> None:
                       "timing": "eager" if args.eager else "hip graph replay"},
            "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
            "frac_of_measured_copy": round(value / copy_bw["GBps"], 4),
-           "step_ms": ms.stats(), "per_shape": per_shape, "roofline": roofline}
+           "step_ms": ms.stats(), "per_shape": per_shape, "roofline": roofline,
+           "portable_row_raw_op": {"ms_per_step": round(ms_port, 4),
+                                   "GBps": round(step_bytes / (ms_port * 1e-3) / 1e9, 1), "per_shape": per_shape_portable,
+                                   "note": "the same ring through w4a16_linear on the portable_row tensors alone (no "
+                                           "prepared copies)"}}
     if not args.no_sweep:
-        out["w4_decode_sweep"], out["w4_prefill"] = bench_w4_sweep(torch, ops, ring, dev, gen, timer, args.steps,
+        out["w4_decode_sweep"], out["w4_prefill"] = bench_w4_sweep(torch, ops, ring, mods, dev, gen, timer, args.steps,
                                                                    args.warmup)
-    del ring
+    del ring, mods
     torch.cuda.empty_cache()
     if not args.no_sweep:
         out["w8a16_decode"] = bench_w8a16(torch, layouts, ops, dev, gen, timer, args.steps, args.warmup)
