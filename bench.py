@@ -361,6 +361,7 @@ def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
               (64 launches of the 8-channel-block GEMV);
     decode -- the CDNA4-layout W4 kernel at M=16 and M=64 on the four Llama-3-8B shapes, over a ring of 6 weights per
               shape, twice (12 launches per shape and M);
+    decode_portable -- the same on the portable_row tensors (the raw op's kernels: skinny / LDS ring + reduce);
     w8a8   -- the FP8 GEMM at M=4096, K=N=8192 and the INT8 GEMM at M=4096, K=8192, N=10240, 5 launches each;
     prefill -- the W4A16 ping-pong prefill kernel at M=8192 on gate+up and down and the W8A16 one on gate+up, 5
               launches each."""
@@ -395,6 +396,19 @@ def pmc_workload(torch, layouts, ops, dev, gen, which: str = "gemv") -> None:
                 torch.cuda.synchronize()
             del ring
         log("pmc workload done: 3 x 256 MiB copy, CDNA4-layout W4 at M=16/64 x 4 shapes x 12 launches")
+    elif which == "decode_portable":
+        for name, (k, n) in SHAPES.items():
+            ring = [make_layer_weights(torch, layouts, dev, k, n, gen) for _ in range(6)]
+            for m in (16, 64):
+                x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+                torch.cuda.synchronize()
+                for _ in range(2):
+                    for p in ring:
+                        ops.w4a16_linear(x, p)
+                torch.cuda.synchronize()
+                log(f"pmc decode_portable {name} M={m}: {ops.last_kernel()}")
+            del ring
+        log("pmc workload done: 3 x 256 MiB copy, portable_row W4 at M=16/64 x 4 shapes x 12 launches")
     elif which == "prefill":
         m = 8192
         for name, bits in (("gate_up", 4), ("down", 4), ("gate_up", 8)):
@@ -528,7 +542,7 @@ def main() -> None:
     ap.add_argument("--no-sweep", action="store_true", help="skip the W4A16 M=4..64 decode and prefill sweeps")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a captured HIP graph")
     ap.add_argument("--pmc-workload", nargs="?", const="gemv", default=None,
-                    choices=("gemv", "decode", "w8a8", "prefill"),
+                    choices=("gemv", "decode", "decode_portable", "w8a8", "prefill"),
                     help="run only a counter-pass workload (no timing): gemv (default), decode or w8a8")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
