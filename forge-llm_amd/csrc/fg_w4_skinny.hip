@@ -81,7 +81,6 @@ __global__ void __launch_bounds__(w4_skinny_max_threads(MB, T)) w4_skinny_kernel
   const int nsteps = K / 128;
   const int st0 = (int)((int64_t)ks * nsteps / KS), st1 = (int)((int64_t)(ks + 1) * nsteps / KS);
   const int r16 = lane & 15, j = lane >> 4;
-  const int64_t ldq4 = ldq / 4;
 
   // per tile: this lane's weight row and the column of its accumulator values (the same channel n0 + 16 t + r16).
   // Offsets are 32-bit from the uniform base pointers (the host checks that every operand spans < 4 GiB).
