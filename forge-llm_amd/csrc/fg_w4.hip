@@ -741,7 +741,8 @@ __global__ void __launch_bounds__(w4_split_max_threads(MT)) w4_gemv_split_kernel
 // Launch shape of the split-K GEMV: S chunks per lane (1 while K <= 32768, else 2 for one row of x), KS =
 // ceil(chunks / (64 S)) K slices (at most 16), R rows per wavefront (16 for one row of x over 8 or more slices, 8 for
 // wide outputs or long K, else 4; R * MT <= 16), BW channel blocks per workgroup (8 .. 16 wavefronts, 8 with four rows of x).  Returns false when the shape is outside its reach (four rows of x: K > 16384).
-bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) {
+// sz8: the scales and zero words come as 8-channel blocks (fg_w4a16_gemv_sz8).
+bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW, bool sz8) {
   const int KW = (K + 7) / 8, KC = (KW + 3) / 4;
   const int s = KC <= 16 * kWave ? 1 : (KC <= 32 * kWave && mt == 1 ? 2 : 0);
   if (s == 0) return false;
@@ -765,8 +766,10 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW) 
   // 8-16 wavefronts otherwise.
   const int nblk = (N + r - 1) / r, cus = device_cus();
   // two rows of x over wide outputs: two channel blocks per workgroup (4-8 wavefronts; M = 2, us, gate+up 15.8 against
-  // 18.6 with the widest workgroups, K = 8192, N = 57344 56.0 against 62.5)
-  int bw = nblk >= 8 * cus ? (mt == 2 ? 2 : max_waves / ks) : max(2, 8 / ks);
+  // 18.6 with the widest workgroups, K = 8192, N = 57344 56.0 against 62.5); one row over wide outputs with the scales
+  // in 8-channel blocks likewise (graph replays, medians of five: gate+up 12.4 against 12.8-13.1 us, K = 8192,
+  // N = 57344 42.6 against 46.4), where the portable scales keep the widest workgroups (gate+up 13.1 against 13.7)
+  int bw = nblk >= 8 * cus ? (mt == 2 || sz8 ? 2 : max_waves / ks) : max(2, 8 / ks);
   if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) bw = nblk / cus;
   while (bw * ks > max_waves && bw > 1) --bw;
   *S = s; *R = r; *KS = ks; *BW = bw;
@@ -846,7 +849,7 @@ hipError_t launch_w4_gemv_split(int mt, bool xbf16, const void* x, int64_t ldx, 
                                 const int32_t* perm, const void* bias, int bdt, void* y, int64_t ldy, int M, int N,
                                 int K, int gs, bool single_group, hipStream_t s) {
   int S, R, KS, BW;
-  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return hipErrorInvalidValue;
+  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW, false)) return hipErrorInvalidValue;
   const int gs32 = single_group ? 0 : gs / 32;
   const bool fast = split_fast(R, x, ldx, perm, scales, sdt, lds, ldq, zeros ? ldz : 0, M, N, K, gs32);
   if (xbf16)
@@ -863,7 +866,7 @@ bool w4_gemv_sz8_ok(const void* x, int64_t ldx, const int32_t* qw, int64_t ldq, 
                     int N, int K, int gs) {
   int S, R, KS, BW;
   const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-  if (M < 1 || M > 4 || !w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return false;
+  if (M < 1 || M > 4 || !w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW, false)) return false;
   const int gs32 = gs > 0 ? gs / 32 : 0;
   if ((gs > 0 && gs % 32 != 0) || N % 8 != 0 || (reinterpret_cast<uintptr_t>(qw) % 16) != 0 || (ldq % 4) != 0)
     return false;
@@ -875,7 +878,7 @@ hipError_t launch_w4_gemv_sz8(int mt, bool xbf16, const void* x, int64_t ldx, co
                               const void* scales8, int sdt, const int32_t* zeros8, const void* bias, int bdt, void* y,
                               int64_t ldy, int M, int N, int K, int gs, bool single_group, hipStream_t s) {
   int S, R, KS, BW;
-  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW)) return hipErrorInvalidValue;
+  if (!w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW, true)) return hipErrorInvalidValue;
   const int gs32 = single_group ? 0 : gs / 32;
   if (xbf16)
     return launch_split_x<true>(mt, S, R, true, true, x, ldx, nullptr, qw, ldq, scales8, sdt, N, zeros8, N / 8, bias,
@@ -886,7 +889,7 @@ hipError_t launch_w4_gemv_sz8(int mt, bool xbf16, const void* x, int64_t ldx, co
 
 bool w4_gemv_split_ok(int mt, int N, int K) {
   int S, R, KS, BW;
-  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW);
+  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW, false);
 }
 
 // Whether the policy takes the split GEMV: its branch-free form applies to these operands, and the shape is not one
@@ -897,7 +900,7 @@ bool w4_gemv_split_preferred(int mt, const void* x, int64_t ldx, const int32_t* 
                              bool single_group) {
   int S, R, KS, BW;
   if (mt == 4 && N / device_cus() >= 64) return false;
-  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW) &&
+  return w4_gemv_split_plan(mt, N, K, &S, &R, &KS, &BW, false) &&
          split_fast(R, x, ldx, perm, scales, sdt, lds, ldq, zeros ? ldz : 0, M, N, K, single_group ? 0 : gs / 32);
 }
 
