@@ -317,8 +317,9 @@ def prepare_w4(packed: PackedW4, layout: Layout | str | None = None) -> PackedW4
 
 # Rows for which a portable_row weight's 8-channel scale blocks (kept by KernelW4A16Linear.prepare) serve the call:
 # the split-K decode GEMV's, which reads them as one contiguous run per wavefront and K slice (graph replays over a
-# 1.2 GB ring, M = 1, us, portable / blocked: qkv 5.13 / 4.89, o_proj 4.31 / 4.26, gate+up 13.84 / 12.91, down 9.16 /
-# 8.59; M = 2 down 11.29 / 10.15), bit-identical results.
+# 1.2 GB ring, M = 1, us, portable / blocked: qkv 5.13 / 4.89, o_proj 4.31 / 4.26, gate+up 13.84 / 12.91 (12.4 once
+# the blocked form took two channel blocks per workgroup), down 9.16 / 8.59; M = 2 down 11.29 / 10.15), bit-identical
+# results.
 SZ8_ROWS = 2
 _SZ8_KEY = "hip.sz8"  # p.meta entry: (tensor stamp, scales8, zeros8)
 
