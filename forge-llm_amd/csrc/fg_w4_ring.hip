@@ -132,6 +132,7 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
   // wavefronts).
   constexpr bool SHARE = Sh::SHARE;
   constexpr float kB = XBF16 ? 128.f : 1024.f;
+  const float zsel = a.hasz ? 1.f : 0.f;  // zero-points present
   constexpr float kCorr8 = XBF16 ? 128.f : 1152.f;  // W8: B = q + 128 (bf16) / 1024 + q + 128 (fp16)
   constexpr uint32_t kOnes = XBF16 ? 0x3F803F80u : 0x3C003C00u;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -260,8 +261,10 @@ __device__ __forceinline__ void ring_body(const RingArgs& a) {
       if constexpr (W8) {
         zb[t] = kCorr8;
       } else {
+        // B + z without a branch (symmetric: zsel = 0 and the zero words read as 0): behind a branch the compiler
+        // waits for this one LDS read before issuing the step's fragment reads
         const uint32_t zw = reinterpret_cast<const uint32_t*>(ssz + 256)[t * 2 + (r16 >> 3)];
-        zb[t] = kB + (a.hasz ? (float)nibble(zw, r16 & 7) : 8.f);
+        zb[t] = __builtin_fmaf(zsel, (float)nibble(zw, r16 & 7) - 8.f, kB + 8.f);
       }
     }
 #pragma unroll
