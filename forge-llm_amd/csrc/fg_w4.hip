@@ -769,7 +769,7 @@ bool w4_gemv_split_plan(int mt, int N, int K, int* S, int* R, int* KS, int* BW, 
   // 18.6 with the widest workgroups, K = 8192, N = 57344 56.0 against 62.5); one row over wide outputs with the scales
   // in 8-channel blocks likewise (graph replays, medians of five: gate+up 12.4 against 12.8-13.1 us, K = 8192,
   // N = 57344 42.6 against 46.4), where the portable scales keep the widest workgroups (gate+up 13.1 against 13.7)
-  int bw = nblk >= 8 * cus ? (mt == 2 || sz8 ? 2 : max_waves / ks) : max(2, 8 / ks);
+  int bw = nblk >= 8 * cus ? (mt == 2 || (sz8 && mt == 1) ? 2 : max_waves / ks) : max(2, 8 / ks);
   if (nblk % cus == 0 && (nblk / cus) * ks <= max_waves) bw = nblk / cus;
   while (bw * ks > max_waves && bw > 1) --bw;
   *S = s; *R = r; *KS = ks; *BW = bw;
